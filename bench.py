@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed-MoE layer on one MI355X.
+
+Workload: BASELINE config 1 by default (K3-shape single-token decode:
+hidden 7168, 896 resident MXFP4 experts, top-16, FFN 2048, SwiGLU, scale
+2.5), seeded synthetic inputs, everything resident in HBM before timing.
+A step is one call of k3_moe_forward_bf16 (router -> top-k -> experts ->
+combine + residual).
+
+Prints one JSON line. `value` is layer tokens/s (wall clock over exactly
+--steps steps, synchronised on both sides). `roofline` is for the dominant
+kernel (decode gate/up for T = 1, timed live with HIP events recorded
+around its stage); `cpu_baseline` is the C oracle of the same layer timed
+on this host's cores on a bounded token sample.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBPS = 8000.0
+MXFP4_PEAK_TFLOPS = 10066.0  # dense MXFP4 MFMA (vendor figure)
+FP8_PEAK_TFLOPS = 5033.0
+BF16_PEAK_TFLOPS = 2516.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Hip:
+    """Just enough of the HIP runtime for events (libamdhip64)."""
+
+    def __init__(self):
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                               ctypes.c_void_p]
+        self.h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        assert self.h.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def elapsed_ms(self, a, b):
+        f = ctypes.c_float()
+        assert self.h.hipEventElapsedTime(ctypes.byref(f), a, b) == 0
+        return f.value
+
+
+def algorithmic_bytes(cfg, T, unique):
+    """Bytes the layer must move: each selected expert once, the router,
+    the bias, hidden/residual/output rows and the routes."""
+    per_expert = 3 * (cfg.ffn * cfg.hidden // 2 + cfg.ffn * cfg.hidden // 32)
+    return (unique * per_expert + cfg.experts * cfg.hidden * 2 + 4 * cfg.experts +
+            3 * T * cfg.hidden * 2 + T * cfg.top_k * 8)
+
+
+def gate_up_bytes(cfg, T, unique):
+    """Bytes of the gate/up stage: gate and up tensors of each selected
+    expert, the hidden rows, the routes and the bf16 activations written."""
+    per = 2 * (cfg.ffn * cfg.hidden // 2 + cfg.ffn * cfg.hidden // 32)
+    return unique * per + T * cfg.hidden * 2 + T * cfg.top_k * (4 + 2 * cfg.ffn)
+
+
+def cpu_baseline(cfg, inputs_cpu, store, budget_s, threads):
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+    import _oracle as O  # CPU checker / baseline only
+    logits = O.router_logits(inputs_cpu.router_weight, inputs_cpu.hidden)
+    ids, _ = O.router_topk(logits, inputs_cpu.router_bias, cfg.top_k, cfg.scale)
+    T = inputs_cpu.hidden.shape[0]
+    done = 0
+    experts = {}
+    t0 = time.perf_counter()
+    while done < T and time.perf_counter() - t0 < budget_s:
+        for e in ids[done]:
+            if int(e) not in experts:
+                experts[int(e)] = store.host_expert(int(e))
+        done += 1
+    gen_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    n = 0
+    while n < done:
+        O.layer(cfg, inputs_cpu, experts, tokens=[n], threads=threads)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} token(s) of {cfg.name} through the C oracle (router, top-k, "
+                      f"{cfg.top_k} MXFP4 experts, combine) with OpenMP over (token, expert) "
+                      f"jobs; {dt:.1f} s (+{gen_s:.1f} s regenerating experts, untimed)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=1, help="BASELINE.json config index")
+    ap.add_argument("--tokens", type=int, default=0, help="override token count")
+    ap.add_argument("--precision", type=int, default=0, help="0 exact, 1 mx8")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
+              "the layer would shard by tensor-parallel F slices (see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from moonshine_amd import layer as L
+    from moonshine_amd._lib import STAGES, K3MoeProfile, lib
+    from moonshine_amd.synth import CONFIGS, make_inputs
+
+    cfg = CONFIGS[args.config]
+    T = args.tokens or cfg.tokens
+    log(f"bench: {cfg.name} T={T} building resident expert store ...")
+    inputs = make_inputs(cfg, tokens=T)
+    moe = L.build_layer(cfg, inputs, device="cuda")
+    x = L.bf16_tensor(inputs.hidden)
+    r = L.bf16_tensor(inputs.residual)
+    out = torch.empty_like(x)
+    ids = torch.zeros((T, cfg.top_k), dtype=torch.int32, device="cuda")
+    wts = torch.zeros((T, cfg.top_k), dtype=torch.float32, device="cuda")
+    ws = moe.workspace(T)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    hip = Hip()
+    profiles = [K3MoeProfile() for _ in range(args.steps)]
+    for p in profiles:
+        for i in range(len(STAGES)):
+            p.stage_events[i] = hip.event().value
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    argv = [P(out), P(x), P(r), P(moe.router_weight), P(moe.router_bias), P(moe.store.table),
+            ctypes.byref(moe.shape), T, args.precision, P(ids), P(wts), P(ws), ws.numel()]
+
+    def step(profile):
+        if not lib().k3_moe_forward_profiled_bf16(*argv, profile, ctypes.c_void_p(stream)):
+            raise RuntimeError("k3_moe_forward_profiled_bf16 failed")
+
+    log(f"bench: warmup {args.warmup} ...")
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    log(f"bench: timing {args.steps} steps ...")
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ctypes.byref(profiles[i]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+
+    stage_ms = {s: 0.0 for s in STAGES[:-1]}
+    gpu_ms = 0.0
+    for p in profiles:
+        ev = list(p.stage_events)
+        for i, s in enumerate(STAGES[:-1]):
+            stage_ms[s] += hip.elapsed_ms(ev[i], ev[i + 1]) / args.steps
+        gpu_ms += hip.elapsed_ms(ev[0], ev[-1]) / args.steps
+
+    ids_h = ids.cpu().numpy()
+    unique = int(np.unique(ids_h).size)
+    total_bytes = algorithmic_bytes(cfg, T, unique)
+    flops = T * cfg.top_k * 2 * 3 * cfg.ffn * cfg.hidden
+    gu_bytes = gate_up_bytes(cfg, T, unique)
+    gu_ms = stage_ms["gate_up"]
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    layer_gbps = total_bytes / (ms_per_step * 1e-3) / 1e9
+    result = {
+        "metric": "routed-MoE layer tok/s; decode HBM GB/s; 8K-prefill MXFP4 TFLOP/s",
+        "value": T / (ms_per_step * 1e-3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 weights, bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded; experts from a counter-based generator, resident in HBM)",
+        "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden,
+                   "experts": cfg.experts, "top_k": cfg.top_k, "ffn": cfg.ffn,
+                   "activation": "swiglu" if cfg.activation == 1 else "situ",
+                   "scale": cfg.scale, "precision": ["exact", "mx8"][args.precision],
+                   "unique_experts": unique},
+        "layer": {"bytes": total_bytes, "hbm_gbps": layer_gbps,
+                  "hbm_frac": layer_gbps / HBM_PEAK_GBPS, "tflops": flops / (ms_per_step * 1e-3) / 1e12,
+                  "gpu_ms_events": gpu_ms, "stage_ms": stage_ms},
+        "roofline": {"kernel": "decode_gateup_kernel" if T == 1 else "grouped_gateup_kernel",
+                     "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "algorithmic_bytes": gu_bytes, "avg_ms": gu_ms},
+    }
+    if not args.no_cpu_baseline:
+        log("bench: CPU baseline (C oracle) ...")
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        cpu_inputs = make_inputs(cfg, tokens=min(T, 64))
+        result["cpu_baseline"] = cpu_baseline(cfg, cpu_inputs, moe.store, args.cpu_budget,
+                                              threads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,179 @@
+#ifndef K3_MOE_H
+#define K3_MOE_H
+
+/*
+ * Routed-MoE layer entry points that have no single counterpart in
+ * Moonshine's k3_rocm_ops.h: they fuse what the engine sequences on the
+ * host in decode_routed_layer (k3_engine.cu:1425-1939) and
+ * prefill_routed_layer / prefill_stream_routed_layer
+ * (k3_engine_prefill.inc:999-1285, 1287-1627), with the routing plan built
+ * on the device instead of by the host loop at
+ * k3_engine_prefill.inc:1175-1194.
+ *
+ * Conventions are those of k3_rocm_ops.h: device pointers, a hipStream_t
+ * passed as void *, arguments validated before any launch (false without
+ * launching), launch errors reported synchronously, execution asynchronous.
+ * Nothing here allocates: the caller passes a workspace of at least
+ * k3_moe_workspace_bytes(). Calls that share a workspace must be ordered on
+ * one stream.
+ */
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * One routed expert in the checkpoint-native MXFP4 layout: packed
+ * [rows, columns / 2] (low nibble = even column) and E8M0 scales
+ * [rows, columns / 32]. Fields follow the six-tensor span order of
+ * k3_prefill.c:71-75 (w1 = gate, w2 = down, w3 = up). Packed pointers must
+ * be 16-byte aligned for the fused kernels.
+ */
+typedef struct {
+    const void *gate_packed;  /* w1.weight_packed [ffn, hidden / 2]  */
+    const void *gate_scales;  /* w1.weight_scale  [ffn, hidden / 32] */
+    const void *down_packed;  /* w2.weight_packed [hidden, ffn / 2]  */
+    const void *down_scales;  /* w2.weight_scale  [hidden, ffn / 32] */
+    const void *up_packed;    /* w3.weight_packed [ffn, hidden / 2]  */
+    const void *up_scales;    /* w3.weight_scale  [ffn, hidden / 32] */
+} k3_moe_expert;
+
+typedef enum {
+    /* beta*tanh(g/beta) * sigmoid(g) * lb*tanh(u/lb): K3's SiTU
+     * (k3_rocm_ops.cu:66-83, beta = 4, lb = 25 at k3_engine.cu:1056). */
+    K3_MOE_ACT_SITU = 0,
+    /* g * sigmoid(g) * u: SiTU's beta, lb -> infinity limit. */
+    K3_MOE_ACT_SWIGLU = 1,
+} k3_moe_activation;
+
+typedef enum {
+    /* Fixed wave64 fp32 orders on the vector ALUs: bit-identical to the
+     * CPU oracle, to the per-matrix k3_rocm_mxfp4_* entry points and
+     * between decode and any batch size. */
+    K3_MOE_EXACT = 0,
+    /* Grouped GEMM on CDNA4 scaled MFMA: weights stay MXFP4, activations are
+     * quantised to MXFP8 (e4m3 + one E8M0 scale per 32 values). */
+    K3_MOE_MX8 = 1,
+} k3_moe_precision;
+
+typedef struct {
+    uint32_t hidden;          /* H: router columns, expert input/output width */
+    uint32_t expert_count;    /* E <= 1024 */
+    uint32_t top_k;           /* k <= 32 */
+    uint32_t ffn;             /* F: expert intermediate width */
+    float    scaling_factor;  /* routed scale (> 0) */
+    uint32_t activation;      /* k3_moe_activation */
+    float    beta;            /* SiTU gate bound (ignored for SwiGLU) */
+    float    linear_beta;     /* SiTU up bound (ignored for SwiGLU) */
+} k3_moe_shape;
+
+/* Bytes of workspace k3_moe_forward_bf16 needs for token_count rows. */
+size_t k3_moe_workspace_bytes(const k3_moe_shape *shape, uint32_t token_count);
+
+/*
+ * Device routing plan (replaces the host loop at
+ * k3_engine_prefill.inc:1175-1194). For every selected expert in
+ * ascending id, rows in (token asc, rank asc) order: a stable sort of the
+ * flattened routes by expert id.
+ *   counts[E], offsets[E + 1], unique[E]      per-expert row counts, their
+ *                                             exclusive scan, selected ids
+ *   summary[4] = {unique count, routes dropped as invalid ids,
+ *                 max rows of one expert, 0}
+ *   token_index[T*k], route_index[T*k]        row -> token, row -> token*k+rank
+ * scratch: at least k3_moe_plan_scratch_bytes(T, E) bytes.
+ */
+size_t k3_moe_plan_scratch_bytes(uint32_t token_count, uint32_t expert_count);
+bool k3_moe_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
+                       uint32_t *summary, uint32_t *token_index,
+                       uint32_t *route_index, const uint32_t *expert_ids,
+                       uint32_t token_count, uint32_t top_k,
+                       uint32_t expert_count, void *scratch,
+                       size_t scratch_bytes, void *stream);
+
+/*
+ * The whole routed-MoE layer for token_count rows:
+ *   logits = router_weight[E, H] . hidden[t]        (f32)
+ *   ids, weights = top-k(sigmoid(logits) + bias)    (k3_rocm_router_topk)
+ *   y[t, r] = down_e(act(gate_e . hidden[t], up_e . hidden[t]))
+ *   output[t] = bf16(residual[t] + bf16(sum_r weights[t, r] * y[t, r]))
+ * residual may be NULL (output is then the combine alone). experts is a
+ * DEVICE array of expert_count descriptors. expert_ids / expert_weights
+ * ([T, k] u32 / f32) are optional extra copies of the routes and may be
+ * host-mapped memory. token_count <= 65535.
+ */
+bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
+                         const void *router_weight, const void *router_bias,
+                         const k3_moe_expert *experts,
+                         const k3_moe_shape *shape, uint32_t token_count,
+                         uint32_t precision, void *expert_ids,
+                         void *expert_weights, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/*
+ * Stage boundaries of k3_moe_forward_profiled_bf16. stage_events[i] (a
+ * hipEvent_t, or NULL) is recorded on the stream just before stage i is
+ * launched; stage_events[K3_MOE_STAGE_END] after the last one. Stages a
+ * call does not run record their event at the same point as the next one.
+ * This is the device-side counterpart of the reference's phase ledger
+ * (k3_engine.h:69-99).
+ */
+enum {
+    K3_MOE_STAGE_ROUTER = 0,   /* router logits */
+    K3_MOE_STAGE_TOPK = 1,     /* top-k + route weights */
+    K3_MOE_STAGE_PLAN = 2,     /* routing plan (T > 1) */
+    K3_MOE_STAGE_GATE_UP = 3,  /* gate/up products + activation */
+    K3_MOE_STAGE_DOWN = 4,     /* down products (T = 1: + combine + residual) */
+    K3_MOE_STAGE_COMBINE = 5,  /* weighted combine + residual (T > 1) */
+    K3_MOE_STAGE_END = 6,
+    K3_MOE_STAGE_COUNT = 7,
+};
+
+typedef struct {
+    void *stage_events[K3_MOE_STAGE_COUNT];
+} k3_moe_profile;
+
+bool k3_moe_forward_profiled_bf16(void *output, const void *hidden,
+                                  const void *residual,
+                                  const void *router_weight,
+                                  const void *router_bias,
+                                  const k3_moe_expert *experts,
+                                  const k3_moe_shape *shape,
+                                  uint32_t token_count, uint32_t precision,
+                                  void *expert_ids, void *expert_weights,
+                                  void *workspace, size_t workspace_bytes,
+                                  const k3_moe_profile *profile, void *stream);
+
+/*
+ * Expert stage only, on routes computed elsewhere (ids/weights [T, k] on
+ * the device): lets the engine keep its own router, and lets tests check
+ * the expert products on identical routes.
+ */
+bool k3_moe_experts_bf16(void *output, const void *hidden, const void *residual,
+                         const void *expert_ids, const void *expert_weights,
+                         const k3_moe_expert *experts,
+                         const k3_moe_shape *shape, uint32_t token_count,
+                         uint32_t precision, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/*
+ * Synthetic resident expert store for benchmarks and tests: fills `bytes`
+ * of device memory at `base` with the counter-based generator
+ * k3_moe_synth_byte(seed, stream, index) below. Packed tensors use uniform
+ * bytes (two uniform e2m1 codes); scale tensors use 121 + (value % 5), i.e.
+ * E8M0 exponents 2^-6 .. 2^-2.
+ */
+bool k3_moe_synth_fill(void *base, uint64_t bytes, uint64_t seed,
+                       uint64_t stream_id, uint32_t kind, void *stream);
+/* Host evaluation of the same generator (kind 0 = packed, 1 = scales). */
+void k3_moe_synth_fill_host(void *base, uint64_t bytes, uint64_t seed,
+                            uint64_t stream_id, uint32_t kind);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

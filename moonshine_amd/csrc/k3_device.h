@@ -1,0 +1,201 @@
+/*
+ * Device helpers shared by the gfx950 kernels of libk3moe.
+ *
+ * Numerics contract: every floating-point step below is written out (fmaf,
+ * separately rounded mul/add; the library is compiled with
+ * -ffp-contract=off), so the fixed "w64" reduction orders produce the same
+ * bits as the CPU oracle that restates them.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k3 {
+
+constexpr uint32_t kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+    return __uint_as_float((uint32_t)v << 16);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+    return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+    return __uint_as_float(w & 0xffff0000u);
+}
+
+/* Round to nearest even; NaN stays a quiet NaN (hip_bfloat16 semantics). */
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* OCP E8M0 as the reference decodes it: 2^(e-127); 0 -> 2^-127 (bit pattern
+ * 0x00400000), 255 -> +inf. */
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+    return __uint_as_float(e == 0u ? 0x00400000u : (e & 0xffu) << 23);
+}
+
+/*
+ * Deterministic exp (Cody-Waite reduction with a two-part ln2, degree-7
+ * Taylor polynomial by Horner with fmaf, exact two-step power-of-two
+ * scaling). The CPU oracle evaluates the same sequence.
+ */
+__device__ __forceinline__ float det_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_huge_valf();
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float n = rintf(__fmul_rn(x, 1.44269502162933349609375f));
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.428606765330187045037746429443359375e-6f, r);
+    float p = 1.9841270113736391067504882812e-4f;
+    p = fmaf(p, r, 1.3888889225199818611145019531e-3f);
+    p = fmaf(p, r, 8.3333337679505348205566406250e-3f);
+    p = fmaf(p, r, 4.1666667908430099487304687500e-2f);
+    p = fmaf(p, r, 1.6666667163372039794921875000e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int a = ni / 2;
+    const int b = ni - a;
+    return __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(a + 127) << 23)),
+                     __uint_as_float((uint32_t)(b + 127) << 23));
+}
+
+__device__ __forceinline__ float det_tanhf(float y) {
+    if (y != y) return y;
+    const float a = fabsf(y);
+    float r;
+    if (a < 0.5f) {
+        const float z = __fmul_rn(a, a);
+        float p = -1.4558343870513183e-3f;
+        p = fmaf(p, z, 3.5921280365724811e-3f);
+        p = fmaf(p, z, -8.8632355299021966e-3f);
+        p = fmaf(p, z, 2.1869488536155203e-2f);
+        p = fmaf(p, z, -5.3968253968253968e-2f);
+        p = fmaf(p, z, 1.3333333333333333e-1f);
+        p = fmaf(p, z, -3.3333333333333333e-1f);
+        r = fmaf(__fmul_rn(a, z), p, a);
+    } else if (a < 9.1f) {
+        const float e = det_expf(__fadd_rn(a, a));
+        r = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(e, 1.0f)));
+    } else {
+        r = 1.0f;
+    }
+    return copysignf(r, y);
+}
+
+__device__ __forceinline__ float det_sigmoid(float x) {
+    return __fdiv_rn(1.0f, __fadd_rn(1.0f, det_expf(-x)));
+}
+
+/* Gated activations on bf16-rounded gate/up values. kind 0 = SiTU(beta, lb)
+ * (k3_rocm_ops.cu:66-83), kind 1 = SwiGLU g*sigmoid(g)*u. */
+__device__ __forceinline__ float gated_act(float g, float u, uint32_t kind,
+                                           float beta, float lb) {
+    if (kind == 1u) return __fmul_rn(__fmul_rn(g, det_sigmoid(g)), u);
+    const float bg = __fmul_rn(beta, det_tanhf(__fdiv_rn(g, beta)));
+    const float bu = __fmul_rn(lb, det_tanhf(__fdiv_rn(u, lb)));
+    return __fmul_rn(__fmul_rn(bg, det_sigmoid(g)), bu);
+}
+
+/* Two e2m1 values of byte `sel` of `w` as fp32, unscaled (exact). */
+template <int Sel>
+__device__ __forceinline__ float2 fp4x2(uint32_t w) {
+    auto v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, Sel);
+    return make_float2(v[0], v[1]);
+}
+
+/*
+ * Sum of 8 e2m1*x products of one packed u32 (8 nibbles, low nibble = even
+ * column) against 8 fp32 activations, accumulated into gs in column order.
+ */
+__device__ __forceinline__ float fp4_dot8(uint32_t w, const float *x, float gs) {
+    float2 a = fp4x2<0>(w), b = fp4x2<1>(w), c = fp4x2<2>(w), d = fp4x2<3>(w);
+    gs = fmaf(a.x, x[0], gs); gs = fmaf(a.y, x[1], gs);
+    gs = fmaf(b.x, x[2], gs); gs = fmaf(b.y, x[3], gs);
+    gs = fmaf(c.x, x[4], gs); gs = fmaf(c.y, x[5], gs);
+    gs = fmaf(d.x, x[6], gs); gs = fmaf(d.y, x[7], gs);
+    return gs;
+}
+
+/* Group partial of one 16-byte (32 column) MXFP4 group. */
+__device__ __forceinline__ float fp4_group(uint4 w, const float *x) {
+    float gs = 0.0f;
+    gs = fp4_dot8(w.x, x, gs);
+    gs = fp4_dot8(w.y, x + 8, gs);
+    gs = fp4_dot8(w.z, x + 16, gs);
+    gs = fp4_dot8(w.w, x + 24, gs);
+    return gs;
+}
+
+/* Unpack 32 bf16 (four uint4) to fp32. */
+__device__ __forceinline__ void bf16x32_to_f32(const uint4 *src, float *x) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint4 v = src[q];
+        x[8 * q + 0] = bf16_lo(v.x); x[8 * q + 1] = bf16_hi(v.x);
+        x[8 * q + 2] = bf16_lo(v.y); x[8 * q + 3] = bf16_hi(v.y);
+        x[8 * q + 4] = bf16_lo(v.z); x[8 * q + 5] = bf16_hi(v.z);
+        x[8 * q + 6] = bf16_lo(v.w); x[8 * q + 7] = bf16_hi(v.w);
+    }
+}
+
+/* Wave64 butterfly: v = v + v(lane ^ o) for o = 32 .. 1 (all lanes end
+ * with the same value). Matches the oracle's butterfly64. */
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+/*
+ * Reduce N per-lane partials (N a power of two, <= 64) over the wave in one
+ * transpose-reduce: at stage o each lane keeps half of its rows and adds
+ * the partner's copy. Every row ends up with exactly the butterfly64 value
+ * (same pairings, fp32 add is commutative). Row i's sum is returned in
+ * lanes whose position selects row i: lane bits (5..) pick the row as
+ * computed by wave_rows_owner().
+ */
+template <int N>
+__device__ __forceinline__ float wave_sum_rows(float (&p)[N]) {
+    const int lane = threadIdx.x & 63;
+    int n = N;
+    int o = 32;
+    /* stages that halve the row set */
+#pragma unroll
+    for (; n > 1 && o >= 1; o >>= 1) {
+        const bool upper = (lane & o) != 0;
+        const int half = n / 2;
+#pragma unroll
+        for (int i = 0; i < half; i++) {
+            const float send = upper ? p[i] : p[i + half];
+            const float keep = upper ? p[i + half] : p[i];
+            const float recv = __shfl_xor(send, o, 64);
+            p[i] = __fadd_rn(keep, recv);
+        }
+        n = half;
+    }
+    float v = p[0];
+    for (; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+/* Which row of wave_sum_rows<N> a lane holds at the end. */
+template <int N>
+__device__ __forceinline__ int wave_rows_owner() {
+    const int lane = threadIdx.x & 63;
+    int row = 0;
+    int n = N;
+    for (int o = 32; n > 1; o >>= 1) {
+        n /= 2;
+        if (lane & o) row += n;
+    }
+    return row;
+}
+
+}  // namespace k3

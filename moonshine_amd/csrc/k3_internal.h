@@ -1,0 +1,39 @@
+/* Launch helpers shared between the translation units of libk3moe. */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k3 {
+
+/* f32 [tokens, rows] = bf16 weights [rows, cols] . bf16 input [tokens, cols]
+ * in the w64 order. */
+bool launch_bf16_rows_f32_any(float *out, const void *weights, const void *input,
+                              uint32_t tokens, uint32_t rows, uint32_t cols,
+                              hipStream_t stream);
+
+/* Router top-k; ids2/w2 (nullable) receive extra copies (e.g. mapped host
+ * memory) while ids/w stay in device memory for later kernels. */
+bool launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,
+                        const float *logits, const float *bias, uint32_t tokens,
+                        uint32_t experts, uint32_t top_k, float scale,
+                        hipStream_t stream);
+
+/* Counter-based generator of the synthetic expert store. */
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+__host__ __device__ inline uint64_t synth_key(uint64_t seed, uint64_t stream_id) {
+    return mix64(seed ^ mix64(stream_id + 0x632be59bd9b4e019ull));
+}
+__host__ __device__ inline uint64_t synth_word(uint64_t key, uint64_t w) {
+    return mix64(key + (w + 1u) * 0x9e3779b97f4a7c15ull);
+}
+__host__ __device__ inline uint8_t synth_byte(uint64_t key, uint64_t i, uint32_t kind) {
+    if (kind == 0u) return (uint8_t)(synth_word(key, i >> 3) >> (8u * (i & 7u)));
+    return (uint8_t)(121u + (uint32_t)((synth_word(key, i) >> 32) % 5u));
+}
+
+}  // namespace k3

@@ -1,0 +1,662 @@
+/*
+ * libk3moe — the fused routed-MoE layer for gfx950.
+ *
+ * Dataflow (replacing decode_routed_layer, k3_engine.cu:1554-1897, and
+ * prefill_routed_layer, k3_engine_prefill.inc:1448-1614, for the
+ * HBM-resident expert store):
+ *
+ *   router logits (bf16 -> f32, w64 order)        k3_rocm_bf16_gemm_f32
+ *   top-k (sigmoid + bias, lowest-id ties)        k3_rocm_router_topk_f32_batch
+ *   T == 1: decode_gateup_kernel   16 experts x F rows, gate and up of a
+ *                                  row in one wave, activation fused
+ *           decode_down_kernel     one block per 8 output rows reads the
+ *                                  row for all k experts and fuses the
+ *                                  weighted combine and the residual add
+ *   T  > 1: device routing plan (count -> scan -> stable scatter), then
+ *           grouped gate/up and down over the selected experts only (each
+ *           expert's weights are read once per row block for all its
+ *           tokens), then the slotted combine.
+ *
+ * No host synchronisation anywhere: the expert ids never leave the device.
+ * Every product uses the per-row w64 order of k3_ops.hip, so the decode and
+ * grouped paths give the same bits for the same token.
+ */
+#include "k3_device.h"
+#include "k3_internal.h"
+#include "../../include/k3_moe.h"
+#include "../../include/k3_rocm_ops.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+using namespace k3;
+
+namespace {
+
+constexpr uint32_t kPlanChunk = 256;  /* tokens per plan block */
+
+inline size_t align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
+
+/* ------------------------------------------------------------------------ */
+/* workspace                                                                 */
+/* ------------------------------------------------------------------------ */
+
+struct Workspace {
+    float *logits;
+    uint32_t *ids;
+    float *weights;
+    uint32_t *counts, *offsets, *unique, *summary;
+    uint32_t *token_index, *route_index;
+    uint32_t *chunk_base;
+    uint16_t *act;
+    uint16_t *y;
+    size_t bytes;
+};
+
+size_t plan_scratch(uint32_t T, uint32_t E) {
+    return align256((size_t)4u * E * ((T + kPlanChunk - 1u) / kPlanChunk));
+}
+
+Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
+    Workspace w{};
+    uint8_t *p = (uint8_t *)base;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t *r = p ? p + off : nullptr;
+        off += align256(bytes);
+        return r;
+    };
+    const uint64_t routes = (uint64_t)T * s.top_k;
+    w.logits = (float *)take(4ull * T * s.expert_count);
+    w.ids = (uint32_t *)take(4ull * routes);
+    w.weights = (float *)take(4ull * routes);
+    w.counts = (uint32_t *)take(4ull * s.expert_count);
+    w.offsets = (uint32_t *)take(4ull * (s.expert_count + 1u));
+    w.unique = (uint32_t *)take(4ull * s.expert_count);
+    w.summary = (uint32_t *)take(16);
+    w.token_index = (uint32_t *)take(4ull * routes);
+    w.route_index = (uint32_t *)take(4ull * routes);
+    w.chunk_base = (uint32_t *)take(plan_scratch(T, s.expert_count));
+    w.act = (uint16_t *)take(2ull * routes * s.ffn);
+    w.y = (uint16_t *)take(T > 1u ? 2ull * routes * s.hidden : 0u);
+    w.bytes = off;
+    return w;
+}
+
+/* ------------------------------------------------------------------------ */
+/* routing plan                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Route (t, r) is valid when its id is < E and no earlier rank of token t
+ * chose the same expert (the router never does; external ids might). */
+__device__ __forceinline__ bool route_valid(const uint32_t *ids, uint32_t t, uint32_t r,
+                                            uint32_t k, uint32_t E) {
+    const uint32_t e = ids[(uint64_t)t * k + r];
+    if (e >= E) return false;
+    for (uint32_t q = 0; q < r; q++)
+        if (ids[(uint64_t)t * k + q] == e) return false;
+    return true;
+}
+
+__global__ __launch_bounds__(256) void plan_count_kernel(uint32_t *__restrict__ chunk_counts,
+                                                         const uint32_t *__restrict__ ids,
+                                                         uint32_t T, uint32_t k, uint32_t E) {
+    __shared__ uint32_t hist[1024];
+    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0u;
+    __syncthreads();
+    const uint32_t t = blockIdx.x * kPlanChunk + threadIdx.x;
+    if (t < T)
+        for (uint32_t r = 0; r < k; r++)
+            if (route_valid(ids, t, r, k, E)) atomicAdd(&hist[ids[(uint64_t)t * k + r]], 1u);
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < E; e += blockDim.x)
+        chunk_counts[(uint64_t)blockIdx.x * E + e] = hist[e];
+}
+
+/* One block of 1024 threads: per-expert scan over chunks, exclusive scan
+ * over experts, compaction of the selected ids. */
+__global__ __launch_bounds__(1024) void plan_scan_kernel(
+        uint32_t *__restrict__ chunk_base, uint32_t *__restrict__ counts,
+        uint32_t *__restrict__ offsets, uint32_t *__restrict__ unique,
+        uint32_t *__restrict__ summary, uint32_t chunks, uint32_t E, uint32_t routes) {
+    __shared__ uint32_t wave_tot[16];
+    __shared__ uint32_t wave_sel[16];
+    __shared__ uint32_t wave_max[16];
+    const uint32_t e = threadIdx.x, lane = e & 63u, wave = e >> 6;
+    uint32_t count = 0u;
+    if (e < E) {
+        for (uint32_t b = 0; b < chunks; b++) {
+            const uint32_t c = chunk_base[(uint64_t)b * E + e];
+            chunk_base[(uint64_t)b * E + e] = count;
+            count += c;
+        }
+    }
+    /* inclusive wave scans of count and of the selected flag */
+    uint32_t inc = count, sel = count ? 1u : 0u, mx = count;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t a = __shfl_up(inc, o, 64), b = __shfl_up(sel, o, 64);
+        if ((int)lane >= o) { inc += a; sel += b; }
+        mx = max(mx, __shfl_xor(mx, o, 64));
+    }
+    if (lane == 63u) { wave_tot[wave] = inc; wave_sel[wave] = sel; }
+    if (lane == 0u) wave_max[wave] = mx;
+    __syncthreads();
+    uint32_t base = 0u, sbase = 0u;
+    for (uint32_t w = 0; w < wave; w++) { base += wave_tot[w]; sbase += wave_sel[w]; }
+    const uint32_t excl = base + inc - count;
+    if (e < E) {
+        counts[e] = count;
+        offsets[e] = excl;
+        if (count) unique[sbase + sel - 1u] = e;
+        for (uint32_t b = 0; b < chunks; b++) chunk_base[(uint64_t)b * E + e] += excl;
+    }
+    if (e == blockDim.x - 1u) {
+        uint32_t total = 0u, nsel = 0u, m = 0u;
+        for (uint32_t w = 0; w < blockDim.x / 64u; w++) {
+            total += wave_tot[w]; nsel += wave_sel[w]; m = max(m, wave_max[w]);
+        }
+        offsets[E] = total;
+        summary[0] = nsel;
+        summary[1] = routes - total;
+        summary[2] = m;
+        summary[3] = 0u;
+    }
+}
+
+__global__ __launch_bounds__(256) void plan_scatter_kernel(
+        uint32_t *__restrict__ token_index, uint32_t *__restrict__ route_index,
+        const uint32_t *__restrict__ chunk_base, const uint32_t *__restrict__ ids, uint32_t T,
+        uint32_t k, uint32_t E) {
+    __shared__ unsigned long long masks[4][1024];
+    for (uint32_t i = threadIdx.x; i < 4u * 1024u; i += blockDim.x) (&masks[0][0])[i] = 0ull;
+    __syncthreads();
+    const uint32_t t = blockIdx.x * kPlanChunk + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (t < T)
+        for (uint32_t r = 0; r < k; r++)
+            if (route_valid(ids, t, r, k, E))
+                atomicOr(&masks[wave][ids[(uint64_t)t * k + r]], 1ull << lane);
+    __syncthreads();
+    if (t >= T) return;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (uint32_t r = 0; r < k; r++) {
+        if (!route_valid(ids, t, r, k, E)) continue;
+        const uint32_t e = ids[(uint64_t)t * k + r];
+        uint32_t before = (uint32_t)__popcll(masks[wave][e] & below);
+        for (uint32_t w = 0; w < wave; w++) before += (uint32_t)__popcll(masks[w][e]);
+        const uint32_t pos = chunk_base[(uint64_t)blockIdx.x * E + e] + before;
+        token_index[pos] = t;
+        route_index[pos] = t * k + r;
+    }
+}
+
+bool launch_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique, uint32_t *summary,
+                 uint32_t *token_index, uint32_t *route_index, uint32_t *chunk_base,
+                 const uint32_t *ids, uint32_t T, uint32_t k, uint32_t E, hipStream_t s) {
+    const uint32_t chunks = (T + kPlanChunk - 1u) / kPlanChunk;
+    hipLaunchKernelGGL(plan_count_kernel, dim3(chunks), dim3(kPlanChunk), 0, s, chunk_base, ids,
+                       T, k, E);
+    hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_base, counts, offsets,
+                       unique, summary, chunks, E, T * k);
+    hipLaunchKernelGGL(plan_scatter_kernel, dim3(chunks), dim3(kPlanChunk), 0, s, token_index,
+                       route_index, chunk_base, ids, T, k, E);
+    return hipGetLastError() == hipSuccess;
+}
+
+/* ------------------------------------------------------------------------ */
+/* decode (one token)                                                        */
+/* ------------------------------------------------------------------------ */
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+/*
+ * grid (F / (4 * RW), k), block 256. Wave w of block b computes rows
+ * [RW*(4b+w), +RW) of both gate and up for expert ids[slot], then applies
+ * the activation to the bf16-rounded pair (k3_engine.cu:1032-1057).
+ * Lane l walks groups l, l+64, ... ; per group the 32 activations are
+ * converted once and reused for all 2*RW rows.
+ */
+template <int RW>
+__global__ __launch_bounds__(256) void decode_gateup_kernel(
+        uint16_t *__restrict__ act, const uint16_t *__restrict__ x,
+        const uint32_t *__restrict__ ids, const k3_moe_expert *__restrict__ experts,
+        uint32_t H, uint32_t F, uint32_t E, uint32_t kind, float beta, float lb) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t slot = blockIdx.y;
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
+    const uint32_t e = ids[slot];
+    if (row0 >= F) return;
+    uint16_t *dst = act + (uint64_t)slot * F + row0;
+    if (e >= E) {
+        if (lane < (uint32_t)RW) dst[lane] = 0;
+        return;
+    }
+    const k3_moe_expert ex = experts[e];
+    const uint32_t G = H / 32u;
+    const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u);
+    const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u);
+    const uint8_t *gsc = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G;
+    const uint8_t *usc = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G;
+    const uint4 *x4 = (const uint4 *)x;
+    float acc[2 * RW];
+#pragma unroll
+    for (int i = 0; i < 2 * RW; i++) acc[i] = 0.0f;
+    for (uint32_t g = lane; g < G; g += 64u) {
+        uint4 w[2 * RW];
+        uint32_t sc[2 * RW];
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            w[i] = *(const uint4 *)(gp + (uint64_t)i * (H / 2u) + 16u * g);
+            w[RW + i] = *(const uint4 *)(up + (uint64_t)i * (H / 2u) + 16u * g);
+            sc[i] = gsc[(uint64_t)i * G + g];
+            sc[RW + i] = usc[(uint64_t)i * G + g];
+        }
+        float xf[32];
+        bf16x32_to_f32(x4 + 4u * g, xf);
+#pragma unroll
+        for (int i = 0; i < 2 * RW; i++)
+            acc[i] = fmaf(fp4_group(w[i], xf), e8m0_to_f32(sc[i]), acc[i]);
+    }
+    const float v = wave_sum_rows<2 * RW>(acc);
+    const float u = __shfl_xor(v, 32, 64);
+    const int owner = wave_rows_owner<2 * RW>();
+    if (lane < 32u && (lane & (64u / (2u * RW) - 1u)) == 0u)
+        dst[owner] = f32_to_bf16(gated_act(bf16_round(v), bf16_round(u), kind, beta, lb));
+}
+
+/*
+ * grid (H / RB), block 64 * k. Wave s computes RB consecutive output rows
+ * of the down projection for slot s; the block then combines the k bf16
+ * slot outputs in rank order and adds the residual (k3_rocm_ops.cu:
+ * 1452-1510 semantics).
+ */
+template <int RB>
+__global__ __launch_bounds__(1024) void decode_down_kernel(
+        uint16_t *__restrict__ out, const uint16_t *__restrict__ act,
+        const uint16_t *__restrict__ residual, const uint32_t *__restrict__ ids,
+        const float *__restrict__ wts, const k3_moe_expert *__restrict__ experts, uint32_t H,
+        uint32_t F, uint32_t E, uint32_t k) {
+    __shared__ float ybuf[32][RB];
+    const uint32_t lane = threadIdx.x & 63u, slot = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * RB;
+    const uint32_t e = ids[slot];
+    const uint32_t G = F / 32u;
+    float acc[RB];
+#pragma unroll
+    for (int i = 0; i < RB; i++) acc[i] = 0.0f;
+    if (e < E) {
+        const k3_moe_expert ex = experts[e];
+        const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
+        const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
+        const uint4 *a4 = (const uint4 *)(act + (uint64_t)slot * F);
+        for (uint32_t g = lane; g < G; g += 64u) {
+            uint4 w[RB];
+            uint32_t sc[RB];
+#pragma unroll
+            for (int i = 0; i < RB; i++) {
+                w[i] = *(const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g);
+                sc[i] = ds[(uint64_t)i * G + g];
+            }
+            float xf[32];
+            bf16x32_to_f32(a4 + 4u * g, xf);
+#pragma unroll
+            for (int i = 0; i < RB; i++)
+                acc[i] = fmaf(fp4_group(w[i], xf), e8m0_to_f32(sc[i]), acc[i]);
+        }
+    }
+    const float v = wave_sum_rows<RB>(acc);
+    const int owner = wave_rows_owner<RB>();
+    if ((lane & (64u / RB - 1u)) == 0u) ybuf[slot][owner] = bf16_round(v);
+    __syncthreads();
+    if (threadIdx.x < (uint32_t)RB) {
+        const uint32_t row = row0 + threadIdx.x;
+        float c = 0.0f;
+        for (uint32_t s = 0; s < k; s++)
+            if (ids[s] < E) c = __fadd_rn(c, __fmul_rn(wts[s], ybuf[s][threadIdx.x]));
+        const float cb = bf16_round(c);
+        out[row] = residual ? f32_to_bf16(__fadd_rn(bf16_to_f32(residual[row]), cb))
+                            : f32_to_bf16(cb);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* grouped (many tokens), exact order                                        */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * grid (F / (4 * RW), E_upper), block 256. blockIdx.y indexes the selected
+ * expert list; blocks beyond the selected count exit. Rows of the plan for
+ * this expert are processed in tiles of TT tokens; the weight group loaded
+ * for a tile is reused by all of its tokens.
+ */
+template <int RW, int TT>
+__global__ __launch_bounds__(256) void grouped_gateup_kernel(
+        uint16_t *__restrict__ act, const uint16_t *__restrict__ x,
+        const uint32_t *__restrict__ unique, const uint32_t *__restrict__ summary,
+        const uint32_t *__restrict__ counts, const uint32_t *__restrict__ offsets,
+        const uint32_t *__restrict__ token_index, const k3_moe_expert *__restrict__ experts,
+        uint32_t H, uint32_t F, uint32_t kind, float beta, float lb) {
+    const uint32_t u = blockIdx.y;
+    if (u >= summary[0]) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
+    if (row0 >= F) return;
+    const uint32_t e = unique[u];
+    const uint32_t n = counts[e], base = offsets[e];
+    const k3_moe_expert ex = experts[e];
+    const uint32_t G = H / 32u;
+    const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u);
+    const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u);
+    const uint8_t *gsc = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G;
+    const uint8_t *usc = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G;
+    for (uint32_t p0 = 0; p0 < n; p0 += TT) {
+        const uint32_t active = n - p0 < (uint32_t)TT ? n - p0 : (uint32_t)TT;
+        uint32_t tok[TT];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+            tok[t] = token_index[base + p0 + ((uint32_t)t < active ? (uint32_t)t : 0u)];
+        float acc[TT][2 * RW];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int i = 0; i < 2 * RW; i++) acc[t][i] = 0.0f;
+        for (uint32_t g = lane; g < G; g += 64u) {
+            uint4 w[2 * RW];
+            float sc[2 * RW];
+#pragma unroll
+            for (int i = 0; i < RW; i++) {
+                w[i] = *(const uint4 *)(gp + (uint64_t)i * (H / 2u) + 16u * g);
+                w[RW + i] = *(const uint4 *)(up + (uint64_t)i * (H / 2u) + 16u * g);
+                sc[i] = e8m0_to_f32(gsc[(uint64_t)i * G + g]);
+                sc[RW + i] = e8m0_to_f32(usc[(uint64_t)i * G + g]);
+            }
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                if ((uint32_t)t < active) {
+                    float xf[32];
+                    bf16x32_to_f32((const uint4 *)(x + (uint64_t)tok[t] * H) + 4u * g, xf);
+#pragma unroll
+                    for (int i = 0; i < 2 * RW; i++)
+                        acc[t][i] = fmaf(fp4_group(w[i], xf), sc[i], acc[t][i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float v = wave_sum_rows<2 * RW>(acc[t]);
+            const float uu = __shfl_xor(v, 32, 64);
+            const int owner = wave_rows_owner<2 * RW>();
+            if ((uint32_t)t < active && lane < 32u && (lane & (64u / (2u * RW) - 1u)) == 0u)
+                act[(uint64_t)(base + p0 + t) * F + row0 + owner] =
+                    f32_to_bf16(gated_act(bf16_round(v), bf16_round(uu), kind, beta, lb));
+        }
+    }
+}
+
+/* grid (H / (4 * RB), E_upper), block 256: y[route] = down_e . act[row]. */
+template <int RB, int TT>
+__global__ __launch_bounds__(256) void grouped_down_kernel(
+        uint16_t *__restrict__ y, const uint16_t *__restrict__ act,
+        const uint32_t *__restrict__ unique, const uint32_t *__restrict__ summary,
+        const uint32_t *__restrict__ counts, const uint32_t *__restrict__ offsets,
+        const uint32_t *__restrict__ route_index, const k3_moe_expert *__restrict__ experts,
+        uint32_t H, uint32_t F) {
+    const uint32_t u = blockIdx.y;
+    if (u >= summary[0]) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RB;
+    if (row0 >= H) return;
+    const uint32_t e = unique[u];
+    const uint32_t n = counts[e], base = offsets[e];
+    const k3_moe_expert ex = experts[e];
+    const uint32_t G = F / 32u;
+    const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
+    const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
+    for (uint32_t p0 = 0; p0 < n; p0 += TT) {
+        const uint32_t active = n - p0 < (uint32_t)TT ? n - p0 : (uint32_t)TT;
+        float acc[TT][RB];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int i = 0; i < RB; i++) acc[t][i] = 0.0f;
+        for (uint32_t g = lane; g < G; g += 64u) {
+            uint4 w[RB];
+            float sc[RB];
+#pragma unroll
+            for (int i = 0; i < RB; i++) {
+                w[i] = *(const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g);
+                sc[i] = e8m0_to_f32(ds[(uint64_t)i * G + g]);
+            }
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                if ((uint32_t)t < active) {
+                    float xf[32];
+                    bf16x32_to_f32((const uint4 *)(act + (uint64_t)(base + p0 + t) * F) + 4u * g, xf);
+#pragma unroll
+                    for (int i = 0; i < RB; i++)
+                        acc[t][i] = fmaf(fp4_group(w[i], xf), sc[i], acc[t][i]);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float v = wave_sum_rows<RB>(acc[t]);
+            const int owner = wave_rows_owner<RB>();
+            if ((uint32_t)t < active && (lane & (64u / RB - 1u)) == 0u)
+                y[(uint64_t)route_index[base + p0 + t] * H + row0 + owner] = f32_to_bf16(v);
+        }
+    }
+}
+
+/* out[t, d] = bf16(residual + bf16(sum_r w[t, r] * y[t*k + r, d])), rank
+ * order, invalid routes skipped. */
+__global__ __launch_bounds__(256) void combine_kernel(
+        uint16_t *__restrict__ out, const uint16_t *__restrict__ y,
+        const uint16_t *__restrict__ residual, const uint32_t *__restrict__ ids,
+        const float *__restrict__ wts, uint32_t H, uint32_t k, uint32_t E) {
+    const uint32_t t = blockIdx.y;
+    for (uint32_t d = blockIdx.x * blockDim.x + threadIdx.x; d < H; d += blockDim.x * gridDim.x) {
+        float c = 0.0f;
+        for (uint32_t r = 0; r < k; r++) {
+            const uint64_t route = (uint64_t)t * k + r;
+            if (ids[route] < E)
+                c = __fadd_rn(c, __fmul_rn(wts[route], bf16_to_f32(y[route * H + d])));
+        }
+        const float cb = bf16_round(c);
+        const uint64_t o = (uint64_t)t * H + d;
+        out[o] = residual ? f32_to_bf16(__fadd_rn(bf16_to_f32(residual[o]), cb)) : f32_to_bf16(cb);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* synthetic store                                                           */
+/* ------------------------------------------------------------------------ */
+
+__global__ void synth_fill_kernel(uint8_t *__restrict__ base, uint64_t bytes, uint64_t key,
+                                  uint32_t kind) {
+    const uint64_t stride = (uint64_t)blockDim.x * gridDim.x;
+    if (kind == 0u) {
+        const uint64_t words = bytes / 8u;
+        for (uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words; w += stride)
+            ((uint64_t *)base)[w] = synth_word(key, w);
+        for (uint64_t i = words * 8u + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes;
+             i += stride)
+            base[i] = synth_byte(key, i, 0u);
+    } else {
+        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes; i += stride)
+            base[i] = synth_byte(key, i, 1u);
+    }
+}
+
+bool shape_ok(const k3_moe_shape *s) {
+    return s && s->hidden && s->hidden % 32u == 0u && s->ffn && s->ffn % 32u == 0u &&
+           s->expert_count && s->expert_count <= 1024u && s->top_k && s->top_k <= 32u &&
+           s->top_k <= s->expert_count && s->scaling_factor > 0.0f && s->activation <= 1u &&
+           (s->activation == 1u || (s->beta > 0.0f && s->linear_beta > 0.0f));
+}
+
+struct Marker {
+    const k3_moe_profile *profile;
+    hipStream_t stream;
+    void operator()(int stage) const {
+        if (profile && profile->stage_events[stage])
+            (void)hipEventRecord((hipEvent_t)profile->stage_events[stage], stream);
+    }
+};
+
+/* Expert stage on routes already in ws.ids / ws.weights. */
+bool run_experts(const Workspace &ws, void *output, const void *hidden, const void *residual,
+                 const k3_moe_expert *experts, const k3_moe_shape &s, uint32_t T,
+                 hipStream_t st, const Marker &mark) {
+    const uint32_t H = s.hidden, F = s.ffn, E = s.expert_count, k = s.top_k;
+    const float beta = s.activation == 1u ? 1.0f : s.beta;
+    const float lb = s.activation == 1u ? 1.0f : s.linear_beta;
+    if (T == 1u && k <= 16u) {
+        mark(K3_MOE_STAGE_PLAN);
+        mark(K3_MOE_STAGE_GATE_UP);
+        constexpr int RW = 4;
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_gateup_kernel<RW>), dim3(F / (4u * RW), k),
+                           dim3(256), 0, st, ws.act, (const uint16_t *)hidden, ws.ids, experts,
+                           H, F, E, s.activation, beta, lb);
+        constexpr int RB = 8;
+        mark(K3_MOE_STAGE_DOWN);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_down_kernel<RB>), dim3(H / RB), dim3(64u * k),
+                           0, st, (uint16_t *)output, ws.act, (const uint16_t *)residual, ws.ids,
+                           ws.weights, experts, H, F, E, k);
+        mark(K3_MOE_STAGE_COMBINE);
+        mark(K3_MOE_STAGE_END);
+        return hipGetLastError() == hipSuccess;
+    }
+    mark(K3_MOE_STAGE_PLAN);
+    if (!launch_plan(ws.counts, ws.offsets, ws.unique, ws.summary, ws.token_index,
+                     ws.route_index, ws.chunk_base, ws.ids, T, k, E, st))
+        return false;
+    const uint32_t upper = (uint64_t)T * k < E ? T * k : E;
+    constexpr int RW = 4, TT = 4, RB = 4;
+    mark(K3_MOE_STAGE_GATE_UP);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_gateup_kernel<RW, TT>), dim3(F / (4u * RW), upper),
+                       dim3(256), 0, st, ws.act, (const uint16_t *)hidden, ws.unique, ws.summary,
+                       ws.counts, ws.offsets, ws.token_index, experts, H, F, s.activation, beta,
+                       lb);
+    mark(K3_MOE_STAGE_DOWN);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TT>), dim3(H / (4u * RB), upper),
+                       dim3(256), 0, st, ws.y, ws.act, ws.unique, ws.summary, ws.counts,
+                       ws.offsets, ws.route_index, experts, H, F);
+    mark(K3_MOE_STAGE_COMBINE);
+    hipLaunchKernelGGL(combine_kernel, dim3((H + 255u) / 256u, T), dim3(256), 0, st,
+                       (uint16_t *)output, ws.y, (const uint16_t *)residual, ws.ids, ws.weights,
+                       H, k, E);
+    mark(K3_MOE_STAGE_END);
+    return hipGetLastError() == hipSuccess;
+}
+
+}  // namespace
+
+/* ======================================================================== */
+/* C ABI                                                                     */
+/* ======================================================================== */
+
+extern "C" size_t k3_moe_workspace_bytes(const k3_moe_shape *shape, uint32_t token_count) {
+    if (!shape_ok(shape) || token_count == 0u || token_count > 65535u) return 0u;
+    return carve(nullptr, *shape, token_count).bytes;
+}
+
+extern "C" size_t k3_moe_plan_scratch_bytes(uint32_t token_count, uint32_t expert_count) {
+    return plan_scratch(token_count, expert_count);
+}
+
+extern "C" bool k3_moe_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
+                                  uint32_t *summary, uint32_t *token_index,
+                                  uint32_t *route_index, const uint32_t *expert_ids,
+                                  uint32_t token_count, uint32_t top_k, uint32_t expert_count,
+                                  void *scratch, size_t scratch_bytes, void *stream) {
+    if (!counts || !offsets || !unique || !summary || !token_index || !route_index ||
+        !expert_ids || !scratch || token_count == 0u || token_count > 65535u || top_k == 0u ||
+        top_k > 32u || expert_count == 0u || expert_count > 1024u ||
+        scratch_bytes < plan_scratch(token_count, expert_count))
+        return false;
+    return launch_plan(counts, offsets, unique, summary, token_index, route_index,
+                       (uint32_t *)scratch, expert_ids, token_count, top_k, expert_count,
+                       (hipStream_t)stream);
+}
+
+extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void *residual,
+                                    const void *expert_ids, const void *expert_weights,
+                                    const k3_moe_expert *experts, const k3_moe_shape *shape,
+                                    uint32_t token_count, uint32_t precision, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+    if (!output || !hidden || !expert_ids || !expert_weights || !experts || !workspace ||
+        !shape_ok(shape) || token_count == 0u || token_count > 65535u || precision != K3_MOE_EXACT)
+        return false;
+    Workspace ws = carve(workspace, *shape, token_count);
+    if (workspace_bytes < ws.bytes) return false;
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t route_bytes = (size_t)token_count * shape->top_k * 4u;
+    if (hipMemcpyAsync(ws.ids, expert_ids, route_bytes, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(ws.weights, expert_weights, route_bytes, hipMemcpyDeviceToDevice, st) !=
+            hipSuccess)
+        return false;
+    return run_experts(ws, output, hidden, residual, experts, *shape, token_count, st,
+                       Marker{nullptr, st});
+}
+
+extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, const void *residual,
+                                    const void *router_weight, const void *router_bias,
+                                    const k3_moe_expert *experts, const k3_moe_shape *shape,
+                                    uint32_t token_count, uint32_t precision, void *expert_ids,
+                                    void *expert_weights, void *workspace,
+                                    size_t workspace_bytes, const k3_moe_profile *profile,
+                                    void *stream) {
+    if (!output || !hidden || !router_weight || !router_bias || !experts || !workspace ||
+        !shape_ok(shape) || token_count == 0u || token_count > 65535u || precision != K3_MOE_EXACT ||
+        ((uintptr_t)hidden % 16u) != 0u)
+        return false;
+    Workspace ws = carve(workspace, *shape, token_count);
+    if (workspace_bytes < ws.bytes) return false;
+    const hipStream_t st = (hipStream_t)stream;
+    const Marker mark{profile, st};
+    mark(K3_MOE_STAGE_ROUTER);
+    if (!launch_bf16_rows_f32_any(ws.logits, router_weight, hidden, token_count,
+                                  shape->expert_count, shape->hidden, st) ||
+        (mark(K3_MOE_STAGE_TOPK), false) ||
+        !launch_router_topk(ws.ids, ws.weights, (uint32_t *)expert_ids, (float *)expert_weights,
+                            ws.logits, (const float *)router_bias, token_count,
+                            shape->expert_count, shape->top_k, shape->scaling_factor, st))
+        return false;
+    return run_experts(ws, output, hidden, residual, experts, *shape, token_count, st, mark);
+}
+
+extern "C" bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
+                                    const void *router_weight, const void *router_bias,
+                                    const k3_moe_expert *experts, const k3_moe_shape *shape,
+                                    uint32_t token_count, uint32_t precision, void *expert_ids,
+                                    void *expert_weights, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+    return k3_moe_forward_profiled_bf16(output, hidden, residual, router_weight, router_bias,
+                                        experts, shape, token_count, precision, expert_ids,
+                                        expert_weights, workspace, workspace_bytes, nullptr,
+                                        stream);
+}
+
+extern "C" bool k3_moe_synth_fill(void *base, uint64_t bytes, uint64_t seed, uint64_t stream_id,
+                                  uint32_t kind, void *stream) {
+    if (!base || bytes == 0u || kind > 1u || ((uintptr_t)base % 8u) != 0u) return false;
+    hipLaunchKernelGGL(synth_fill_kernel, dim3(2048), dim3(256), 0, (hipStream_t)stream,
+                       (uint8_t *)base, bytes, synth_key(seed, stream_id), kind);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" void k3_moe_synth_fill_host(void *base, uint64_t bytes, uint64_t seed,
+                                       uint64_t stream_id, uint32_t kind) {
+    const uint64_t key = synth_key(seed, stream_id);
+    uint8_t *p = (uint8_t *)base;
+    uint64_t i = 0;
+    if (kind == 0u)
+        for (; i + 8u <= bytes; i += 8u) {
+            const uint64_t w = synth_word(key, i >> 3);
+            memcpy(p + i, &w, 8);
+        }
+    for (; i < bytes; i++) p[i] = synth_byte(key, i, kind);
+}

@@ -1,0 +1,502 @@
+/*
+ * libk3moe — gfx950 kernels behind the routed-MoE entry points that
+ * Moonshine declares in k3_rocm_ops.h. Signatures, argument validation and
+ * return conventions follow the reference launchers; the kernels are
+ * written for CDNA4 wave64.
+ *
+ * Reduction orders ("w64"):
+ *   bf16 -> f32 rows: elements in chunks of 8, lane l owns chunks l, l+64,
+ *     ..., acc = fmaf(w, x, acc) in column order, then a wave64 butterfly.
+ *   MXFP4 rows: lane l owns 32-column groups l, l+64, ...; each group is
+ *     gs = fmaf(e2m1, x, gs) over its 32 columns, then acc = fmaf(gs,
+ *     2^(e-127), acc); wave64 butterfly; bf16 round.
+ * Every token row of a batch uses the same order as the single-vector form,
+ * so batch == sequential and results do not depend on the batch tile.
+ */
+#include "k3_device.h"
+#include "k3_internal.h"
+#include "../../include/k3_rocm_ops.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+using namespace k3;
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr uint32_t kWavesPerBlock = kThreads / kWave;
+
+inline uint32_t grid_cap(uint64_t blocks) {
+    return (uint32_t)(blocks > 65535u ? 65535u : (blocks ? blocks : 1u));
+}
+
+/* ------------------------------------------------------------------------ */
+/* bf16 weights x bf16 inputs -> f32 (router logits)                         */
+/* ------------------------------------------------------------------------ */
+
+template <int TT>
+__global__ __launch_bounds__(256) void bf16_rows_f32_kernel(
+        float *__restrict__ out, const uint16_t *__restrict__ weights,
+        const uint16_t *__restrict__ input, uint32_t tokens, uint32_t rows,
+        uint32_t cols, uint32_t vec_ok) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const uint32_t t0 = blockIdx.y * TT;
+    if (row >= rows) return;
+    const uint32_t active = tokens - t0 < (uint32_t)TT ? tokens - t0 : (uint32_t)TT;
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.0f;
+    const uint16_t *w = weights + (uint64_t)row * cols;
+    const uint32_t chunks = (cols + 7u) / 8u;
+    if (vec_ok) {
+        const uint4 *w4 = (const uint4 *)w;
+        for (uint32_t c = lane; c < chunks; c += 64u) {
+            const uint4 wv = w4[c];
+            const float wf[8] = {bf16_lo(wv.x), bf16_hi(wv.x), bf16_lo(wv.y), bf16_hi(wv.y),
+                                 bf16_lo(wv.z), bf16_hi(wv.z), bf16_lo(wv.w), bf16_hi(wv.w)};
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                if ((uint32_t)t < active) {
+                    const uint4 xv = ((const uint4 *)(input + (uint64_t)(t0 + t) * cols))[c];
+                    float a = acc[t];
+                    a = fmaf(wf[0], bf16_lo(xv.x), a); a = fmaf(wf[1], bf16_hi(xv.x), a);
+                    a = fmaf(wf[2], bf16_lo(xv.y), a); a = fmaf(wf[3], bf16_hi(xv.y), a);
+                    a = fmaf(wf[4], bf16_lo(xv.z), a); a = fmaf(wf[5], bf16_hi(xv.z), a);
+                    a = fmaf(wf[6], bf16_lo(xv.w), a); a = fmaf(wf[7], bf16_hi(xv.w), a);
+                    acc[t] = a;
+                }
+            }
+        }
+    } else {
+        for (uint32_t c = lane; c < chunks; c += 64u) {
+            const uint32_t end = 8u * c + 8u < cols ? 8u * c + 8u : cols;
+            for (uint32_t i = 8u * c; i < end; i++) {
+                const float wf = bf16_to_f32(w[i]);
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+                    if ((uint32_t)t < active)
+                        acc[t] = fmaf(wf, bf16_to_f32(input[(uint64_t)(t0 + t) * cols + i]), acc[t]);
+            }
+        }
+    }
+    const float v = wave_sum_rows<TT>(acc);
+    const int owner = wave_rows_owner<TT>();
+    if ((lane & (64u / TT - 1u)) == 0u && (uint32_t)owner < active)
+        out[(uint64_t)(t0 + owner) * rows + row] = v;
+}
+
+template <int TT>
+bool launch_bf16_rows_f32(void *out, const void *w, const void *x, uint32_t tokens,
+                          uint32_t rows, uint32_t cols, hipStream_t s) {
+    const uint32_t vec_ok = (cols % 8u == 0u) && (((uintptr_t)w | (uintptr_t)x) % 16u == 0u);
+    dim3 grid((rows + kWavesPerBlock - 1u) / kWavesPerBlock, (tokens + TT - 1u) / TT);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(bf16_rows_f32_kernel<TT>), grid, dim3(kThreads), 0, s,
+                       (float *)out, (const uint16_t *)w, (const uint16_t *)x, tokens, rows,
+                       cols, vec_ok);
+    return hipGetLastError() == hipSuccess;
+}
+
+/* ------------------------------------------------------------------------ */
+/* router top-k                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* (choice desc, id asc) total order; NaN choices never win. */
+__device__ __forceinline__ bool better(float c, uint32_t id, float bc, uint32_t bid) {
+    if (c != c) return false;
+    if (bid == UINT32_MAX) return true;
+    return c > bc || (c == bc && id < bid);
+}
+
+/*
+ * One block per token. Scores and choices are computed once per expert,
+ * then top_k rounds of a block-wide arg-max under (choice desc, id asc)
+ * produce the ids in rank order; this is the same order as the reference's
+ * bitonic sort read from the end (k3_rocm_ops.cu:1397-1437).
+ */
+__global__ __launch_bounds__(256) void router_topk_kernel(
+        uint32_t *__restrict__ ids_out, float *__restrict__ w_out,
+        uint32_t *ids_copy, float *w_copy,
+        const float *__restrict__ logits, const float *__restrict__ bias,
+        uint32_t experts, uint32_t top_k, float scale) {
+    __shared__ float s_score[1024];
+    __shared__ float s_choice[1024];
+    __shared__ float r_choice[4];
+    __shared__ uint32_t r_id[4];
+    __shared__ uint32_t sel_id[64];
+    __shared__ float sel_score[64];
+    const uint32_t t = blockIdx.x;
+    const float *lg = logits + (uint64_t)t * experts;
+    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
+        const float s = det_sigmoid(lg[e]);
+        s_score[e] = s;
+        s_choice[e] = __fadd_rn(s, bias[e]);
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    for (uint32_t r = 0; r < top_k; r++) {
+        float bc = 0.0f;
+        uint32_t bid = UINT32_MAX;
+        for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x)
+            if (better(s_choice[e], e, bc, bid)) { bc = s_choice[e]; bid = e; }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float oc = __shfl_xor(bc, o, 64);
+            const uint32_t oid = __shfl_xor(bid, o, 64);
+            if (oid != UINT32_MAX && better(oc, oid, bc, bid)) { bc = oc; bid = oid; }
+        }
+        if (lane == 0u) { r_choice[wave] = bc; r_id[wave] = bid; }
+        __syncthreads();
+        if (threadIdx.x == 0u) {
+            float c = r_choice[0];
+            uint32_t id = r_id[0];
+            for (uint32_t w = 1; w < blockDim.x / 64u; w++)
+                if (r_id[w] != UINT32_MAX && better(r_choice[w], r_id[w], c, id)) {
+                    c = r_choice[w]; id = r_id[w];
+                }
+            sel_id[r] = id;
+            sel_score[r] = id == UINT32_MAX ? 0.0f : s_score[id];
+            if (id != UINT32_MAX) s_choice[id] = __builtin_nanf("");
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0u) {
+        float den = 1e-20f;
+        for (uint32_t r = 0; r < top_k; r++) den = __fadd_rn(den, sel_score[r]);
+        for (uint32_t r = 0; r < top_k; r++) {
+            const float wr = __fmul_rn(__fdiv_rn(sel_score[r], den), scale);
+            ids_out[(uint64_t)t * top_k + r] = sel_id[r];
+            w_out[(uint64_t)t * top_k + r] = wr;
+            if (ids_copy) ids_copy[(uint64_t)t * top_k + r] = sel_id[r];
+            if (w_copy) w_copy[(uint64_t)t * top_k + r] = wr;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* MXFP4 rows (generic GEMV / GEMM behind the reference ABI)                 */
+/* ------------------------------------------------------------------------ */
+
+__device__ __forceinline__ uint4 load_group(const uint8_t *p, uint32_t align16) {
+    if (align16) return *(const uint4 *)p;
+    /* 8-byte aligned starts occur in real checkpoints (k3_rocm_ops.cu:207-223). */
+    const uint2 a = ((const uint2 *)p)[0], b = ((const uint2 *)p)[1];
+    return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+template <int TT>
+__global__ __launch_bounds__(256) void mxfp4_rows_kernel(
+        uint16_t *__restrict__ out, const uint8_t *__restrict__ packed,
+        const uint8_t *__restrict__ scales, const uint16_t *__restrict__ input,
+        uint32_t tokens, uint32_t rows, uint32_t cols, uint32_t align16) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const uint32_t t0 = blockIdx.y * TT;
+    if (row >= rows) return;
+    const uint32_t active = tokens - t0 < (uint32_t)TT ? tokens - t0 : (uint32_t)TT;
+    const uint32_t groups = cols / 32u;
+    const uint8_t *prow = packed + (uint64_t)row * (cols / 2u);
+    const uint8_t *srow = scales + (uint64_t)row * groups;
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.0f;
+    for (uint32_t g = lane; g < groups; g += 64u) {
+        const uint4 wv = load_group(prow + 16u * g, align16);
+        const float sc = e8m0_to_f32(srow[g]);
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            if ((uint32_t)t < active) {
+                float xf[32];
+                bf16x32_to_f32((const uint4 *)(input + (uint64_t)(t0 + t) * cols) + 4u * g, xf);
+                acc[t] = fmaf(fp4_group(wv, xf), sc, acc[t]);
+            }
+        }
+    }
+    const float v = wave_sum_rows<TT>(acc);
+    const int owner = wave_rows_owner<TT>();
+    if ((lane & (64u / TT - 1u)) == 0u && (uint32_t)owner < active)
+        out[(uint64_t)(t0 + owner) * rows + row] = f32_to_bf16(v);
+}
+
+template <int TT>
+bool launch_mxfp4_rows(void *out, const void *p, const void *s, const void *x,
+                       uint32_t tokens, uint32_t rows, uint32_t cols, hipStream_t st) {
+    const uint32_t align16 = ((uintptr_t)p % 16u) == 0u;
+    dim3 grid((rows + kWavesPerBlock - 1u) / kWavesPerBlock, (tokens + TT - 1u) / TT);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(mxfp4_rows_kernel<TT>), grid, dim3(kThreads), 0, st,
+                       (uint16_t *)out, (const uint8_t *)p, (const uint8_t *)s,
+                       (const uint16_t *)x, tokens, rows, cols, align16);
+    return hipGetLastError() == hipSuccess;
+}
+
+/* ------------------------------------------------------------------------ */
+/* elementwise                                                               */
+/* ------------------------------------------------------------------------ */
+
+__global__ void gated_act_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ gate,
+                                 const uint16_t *__restrict__ up, uint64_t n, uint32_t kind,
+                                 float beta, float lb) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)blockDim.x * gridDim.x)
+        out[i] = f32_to_bf16(gated_act(bf16_to_f32(gate[i]), bf16_to_f32(up[i]), kind, beta, lb));
+}
+
+/* out[t, d] = bf16(sum_r w[t, r] * v[t, r, d]) in rank order, products and
+ * sums rounded separately (k3_rocm_ops.cu:1452-1474). */
+__global__ void weighted_sum_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ v,
+                                    const float *__restrict__ w, uint32_t count, uint32_t hidden) {
+    const uint32_t t = blockIdx.y;
+    const uint16_t *vt = v + (uint64_t)t * count * hidden;
+    const float *wt = w + (uint64_t)t * count;
+    for (uint32_t d = blockIdx.x * blockDim.x + threadIdx.x; d < hidden; d += blockDim.x * gridDim.x) {
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < count; r++)
+            sum = __fadd_rn(sum, __fmul_rn(wt[r], bf16_to_f32(vt[(uint64_t)r * hidden + d])));
+        out[(uint64_t)t * hidden + d] = f32_to_bf16(sum);
+    }
+}
+
+template <bool Scatter>
+__global__ void copy_rows_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ in,
+                                 const uint32_t *__restrict__ ids, uint32_t row_count,
+                                 uint32_t row_size) {
+    const uint64_t n = (uint64_t)row_count * row_size;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)blockDim.x * gridDim.x) {
+        const uint32_t r = (uint32_t)(i / row_size), c = (uint32_t)(i % row_size);
+        const uint64_t j = (uint64_t)ids[r] * row_size + c;
+        if (Scatter) out[j] = in[i];
+        else out[i] = in[j];
+    }
+}
+
+__global__ void add_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ a,
+                           const uint16_t *__restrict__ b, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)blockDim.x * gridDim.x)
+        out[i] = f32_to_bf16(__fadd_rn(bf16_to_f32(a[i]), bf16_to_f32(b[i])));
+}
+
+__global__ void rms_norm_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ in,
+                                const uint16_t *__restrict__ weight, uint32_t hidden, float eps) {
+    __shared__ float part[4];
+    const uint16_t *x = in + (uint64_t)blockIdx.x * hidden;
+    float s = 0.0f;
+    for (uint32_t d = threadIdx.x; d < hidden; d += blockDim.x) {
+        const float v = bf16_to_f32(x[d]);
+        s = fmaf(v, v, s);
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float total = __fadd_rn(__fadd_rn(part[0], part[1]), __fadd_rn(part[2], part[3]));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)hidden), eps)));
+    for (uint32_t d = threadIdx.x; d < hidden; d += blockDim.x)
+        out[(uint64_t)blockIdx.x * hidden + d] =
+            f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(x[d]), inv), bf16_to_f32(weight[d])));
+}
+
+}  // namespace
+
+bool k3::launch_bf16_rows_f32_any(float *out, const void *w, const void *x, uint32_t tokens,
+                                  uint32_t rows, uint32_t cols, hipStream_t s) {
+    if (tokens == 1u) return launch_bf16_rows_f32<1>(out, w, x, 1u, rows, cols, s);
+    if (tokens <= 4u) return launch_bf16_rows_f32<4>(out, w, x, tokens, rows, cols, s);
+    return launch_bf16_rows_f32<16>(out, w, x, tokens, rows, cols, s);
+}
+
+bool k3::launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,
+                            const float *logits, const float *bias, uint32_t tokens,
+                            uint32_t experts, uint32_t top_k, float scale, hipStream_t s) {
+    hipLaunchKernelGGL(router_topk_kernel, dim3(tokens), dim3(256), 0, s, ids, w, ids2, w2,
+                       logits, bias, experts, top_k, scale);
+    return hipGetLastError() == hipSuccess;
+}
+
+/* ======================================================================== */
+/* C ABI                                                                     */
+/* ======================================================================== */
+
+extern "C" bool k3_rocm_situ_bf16(void *output, const void *gate, const void *up,
+                                  uint64_t element_count, float beta, float linear_beta,
+                                  void *stream) {
+    if (!output || !gate || !up || element_count == 0u || !(beta > 0.0f) ||
+        !(linear_beta > 0.0f))
+        return false;
+    hipLaunchKernelGGL(gated_act_kernel, dim3(grid_cap((element_count + 255u) / 256u)),
+                       dim3(256), 0, (hipStream_t)stream, (uint16_t *)output,
+                       (const uint16_t *)gate, (const uint16_t *)up, element_count, 0u, beta,
+                       linear_beta);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_rocm_swiglu_bf16(void *output, const void *gate, const void *up,
+                                    uint64_t element_count, void *stream) {
+    if (!output || !gate || !up || element_count == 0u) return false;
+    hipLaunchKernelGGL(gated_act_kernel, dim3(grid_cap((element_count + 255u) / 256u)),
+                       dim3(256), 0, (hipStream_t)stream, (uint16_t *)output,
+                       (const uint16_t *)gate, (const uint16_t *)up, element_count, 1u, 1.0f,
+                       1.0f);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_rocm_mxfp4_gemm_tiled_bf16(void *output, const void *packed,
+                                              const void *scales, const void *input,
+                                              uint32_t vector_count, uint32_t rows,
+                                              uint32_t columns, uint32_t batch_tile,
+                                              void *stream) {
+    if (!output || !packed || !scales || !input || vector_count == 0u ||
+        vector_count > 65535u || rows == 0u || columns == 0u || columns % 32u != 0u ||
+        ((uintptr_t)packed % 8u) != 0u || ((uintptr_t)input % 16u) != 0u)
+        return false;
+    const hipStream_t s = (hipStream_t)stream;
+    switch (batch_tile) {
+        case 16u: return launch_mxfp4_rows<16>(output, packed, scales, input, vector_count, rows, columns, s);
+        case 32u: return launch_mxfp4_rows<32>(output, packed, scales, input, vector_count, rows, columns, s);
+        case 64u: return launch_mxfp4_rows<64>(output, packed, scales, input, vector_count, rows, columns, s);
+        default: return false;
+    }
+}
+
+extern "C" bool k3_rocm_mxfp4_gemm_bf16(void *output, const void *packed, const void *scales,
+                                        const void *input, uint32_t vector_count, uint32_t rows,
+                                        uint32_t columns, void *stream) {
+    if (!output || !packed || !scales || !input || vector_count == 0u ||
+        vector_count > 65535u || rows == 0u || columns == 0u || columns % 32u != 0u ||
+        ((uintptr_t)packed % 8u) != 0u || ((uintptr_t)input % 16u) != 0u)
+        return false;
+    const hipStream_t s = (hipStream_t)stream;
+    if (vector_count == 1u)
+        return launch_mxfp4_rows<1>(output, packed, scales, input, 1u, rows, columns, s);
+    if (vector_count <= 4u)
+        return launch_mxfp4_rows<4>(output, packed, scales, input, vector_count, rows, columns, s);
+    return launch_mxfp4_rows<16>(output, packed, scales, input, vector_count, rows, columns, s);
+}
+
+extern "C" bool k3_rocm_mxfp4_gemv_bf16(void *output, const void *packed, const void *scales,
+                                        const void *input, uint32_t rows, uint32_t columns,
+                                        void *stream) {
+    return k3_rocm_mxfp4_gemm_bf16(output, packed, scales, input, 1u, rows, columns, stream);
+}
+
+extern "C" bool k3_rocm_bf16_gemm_tiled_f32(void *output, const void *weights,
+                                            const void *input, uint32_t vector_count,
+                                            uint32_t rows, uint32_t columns,
+                                            uint32_t batch_tile, void *stream) {
+    if (!output || !weights || !input || vector_count == 0u || vector_count > 65535u ||
+        rows == 0u || columns == 0u)
+        return false;
+    const hipStream_t s = (hipStream_t)stream;
+    switch (batch_tile) {
+        case 16u: return launch_bf16_rows_f32<16>(output, weights, input, vector_count, rows, columns, s);
+        case 32u: return launch_bf16_rows_f32<32>(output, weights, input, vector_count, rows, columns, s);
+        case 64u: return launch_bf16_rows_f32<64>(output, weights, input, vector_count, rows, columns, s);
+        default: return false;
+    }
+}
+
+extern "C" bool k3_rocm_bf16_gemm_f32(void *output, const void *weights, const void *input,
+                                      uint32_t vector_count, uint32_t rows, uint32_t columns,
+                                      void *stream) {
+    if (!output || !weights || !input || vector_count == 0u || vector_count > 65535u ||
+        rows == 0u || columns == 0u)
+        return false;
+    return k3::launch_bf16_rows_f32_any((float *)output, weights, input, vector_count, rows,
+                                        columns, (hipStream_t)stream);
+}
+
+extern "C" bool k3_rocm_bf16_gemv_f32(void *output, const void *weights, const void *input,
+                                      uint32_t rows, uint32_t columns, void *stream) {
+    return k3_rocm_bf16_gemm_f32(output, weights, input, 1u, rows, columns, stream);
+}
+
+extern "C" bool k3_rocm_router_topk_f32_batch(void *expert_ids, void *expert_weights,
+                                              const void *logits, const void *correction_bias,
+                                              uint32_t vector_count, uint32_t expert_count,
+                                              uint32_t top_k, float scaling_factor,
+                                              void *stream) {
+    if (!expert_ids || !expert_weights || !logits || !correction_bias || vector_count == 0u ||
+        vector_count > 65535u || expert_count == 0u || top_k == 0u || top_k > expert_count ||
+        expert_count > 1024u || top_k > 32u || !(scaling_factor > 0.0f))
+        return false;
+    return k3::launch_router_topk((uint32_t *)expert_ids, (float *)expert_weights, nullptr,
+                                  nullptr, (const float *)logits,
+                                  (const float *)correction_bias, vector_count, expert_count,
+                                  top_k, scaling_factor, (hipStream_t)stream);
+}
+
+extern "C" bool k3_rocm_router_topk_f32(void *expert_ids, void *expert_weights,
+                                        const void *logits, const void *correction_bias,
+                                        uint32_t expert_count, uint32_t top_k,
+                                        float scaling_factor, void *stream) {
+    return k3_rocm_router_topk_f32_batch(expert_ids, expert_weights, logits, correction_bias, 1u,
+                                         expert_count, top_k, scaling_factor, stream);
+}
+
+extern "C" bool k3_rocm_weighted_sum_bf16_batch(void *output, const void *vectors,
+                                                const void *weights, uint32_t token_count,
+                                                uint32_t vector_count, uint32_t hidden_size,
+                                                void *stream) {
+    if (!output || !vectors || !weights || token_count == 0u || token_count > 65535u ||
+        vector_count == 0u || hidden_size == 0u)
+        return false;
+    hipLaunchKernelGGL(weighted_sum_kernel, dim3((hidden_size + 255u) / 256u, token_count),
+                       dim3(256), 0, (hipStream_t)stream, (uint16_t *)output,
+                       (const uint16_t *)vectors, (const float *)weights, vector_count,
+                       hidden_size);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_rocm_weighted_sum_bf16(void *output, const void *vectors, const void *weights,
+                                          uint32_t vector_count, uint32_t hidden_size,
+                                          void *stream) {
+    return k3_rocm_weighted_sum_bf16_batch(output, vectors, weights, 1u, vector_count,
+                                           hidden_size, stream);
+}
+
+static bool copy_rows(bool scatter, void *output, const void *input, const void *row_ids,
+                      uint32_t row_count, uint32_t row_size, void *stream) {
+    if (!output || !input || !row_ids || row_count == 0u || row_size == 0u) return false;
+    const uint64_t n = (uint64_t)row_count * row_size;
+    const dim3 grid(grid_cap((n + 255u) / 256u));
+    if (scatter)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(copy_rows_kernel<true>), grid, dim3(256), 0,
+                           (hipStream_t)stream, (uint16_t *)output, (const uint16_t *)input,
+                           (const uint32_t *)row_ids, row_count, row_size);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(copy_rows_kernel<false>), grid, dim3(256), 0,
+                           (hipStream_t)stream, (uint16_t *)output, (const uint16_t *)input,
+                           (const uint32_t *)row_ids, row_count, row_size);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_rocm_gather_rows_bf16(void *output, const void *input, const void *row_ids,
+                                         uint32_t row_count, uint32_t row_size, void *stream) {
+    return copy_rows(false, output, input, row_ids, row_count, row_size, stream);
+}
+
+extern "C" bool k3_rocm_scatter_rows_bf16(void *output, const void *input, const void *row_ids,
+                                          uint32_t row_count, uint32_t row_size, void *stream) {
+    return copy_rows(true, output, input, row_ids, row_count, row_size, stream);
+}
+
+extern "C" bool k3_rocm_add_bf16(void *output, const void *left, const void *right,
+                                 uint64_t element_count, void *stream) {
+    if (!output || !left || !right || element_count == 0u) return false;
+    hipLaunchKernelGGL(add_kernel, dim3(grid_cap((element_count + 255u) / 256u)), dim3(256), 0,
+                       (hipStream_t)stream, (uint16_t *)output, (const uint16_t *)left,
+                       (const uint16_t *)right, element_count);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_rocm_rms_norm_bf16(void *output, const void *input, const void *weight,
+                                      uint32_t vector_count, uint32_t hidden_size, float epsilon,
+                                      void *stream) {
+    if (!output || !input || !weight || vector_count == 0u || hidden_size == 0u) return false;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(vector_count), dim3(256), 0, (hipStream_t)stream,
+                       (uint16_t *)output, (const uint16_t *)input, (const uint16_t *)weight,
+                       hidden_size, epsilon);
+    return hipGetLastError() == hipSuccess;
+}

@@ -1,0 +1,584 @@
+/*
+ * k3moe_oracle.c — CPU restatement of Moonshine's routed-MoE layer.
+ * TEST INFRASTRUCTURE ONLY (see k3moe_oracle.h). Built with
+ * -ffp-contract=off and without -ffast-math so every rounding is the one
+ * written here.
+ */
+#include "k3moe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* scalars                                                                   */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* bf16 <-> f32: hip_bfloat16 semantics (round to nearest even, NaN kept
+ * quiet), as used by the reference via k3_float_to_bf16 (k3_rocm_ops.cu:36-39). */
+float k3o_bf16_to_f32(uint16_t v) { return u2f((uint32_t)v << 16); }
+
+uint16_t k3o_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* e2m1: {0, .5, 1, 1.5, 2, 3, 4, 6}, bit 3 = sign (k3_rocm_ops.cu:185-191). */
+float k3o_e2m1(uint8_t nibble) {
+    static const float magnitude[8] = {0.0f, 0.5f, 1.0f, 1.5f,
+                                       2.0f, 3.0f, 4.0f, 6.0f};
+    const float v = magnitude[nibble & 7u];
+    return (nibble & 8u) ? -v : v;
+}
+
+/* e8m0: 2^(e-127); e = 0 gives the bit pattern 0x00400000 (2^-127) and
+ * e = 255 gives +inf, exactly as k3_rocm_ops.cu:179-183. */
+float k3o_e8m0(uint8_t e) {
+    return u2f(e == 0u ? 0x00400000u : (uint32_t)e << 23);
+}
+
+/*
+ * Deterministic exp: Cody-Waite reduction x = n ln2 + r with a two-part ln2,
+ * then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2 evaluated by
+ * Horner with fmaf, then an exact two-step power-of-two scaling. The HIP
+ * kernels evaluate the identical sequence, so sigmoid scores (and therefore
+ * routing) agree bit for bit. Accuracy vs glibc expf is pinned in tests.
+ */
+float k3o_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541015625f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.428606765330187045037746429443359375e-6f, r);
+    float p = 1.9841270113736391067504882812e-4f;        /* 1/7! */
+    p = fmaf(p, r, 1.3888889225199818611145019531e-3f);  /* 1/6! */
+    p = fmaf(p, r, 8.3333337679505348205566406250e-3f);  /* 1/5! */
+    p = fmaf(p, r, 4.1666667908430099487304687500e-2f);  /* 1/4! */
+    p = fmaf(p, r, 1.6666667163372039794921875000e-1f);  /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int a = ni / 2;
+    const int b = ni - a;
+    return (p * u2f((uint32_t)(a + 127) << 23)) * u2f((uint32_t)(b + 127) << 23);
+}
+
+/* Deterministic tanh: odd Taylor series through a^15 for |a| < 0.5, else
+ * 1 - 2/(e^{2a}+1) with k3o_expf, saturating to 1 for |a| >= 9.1. */
+float k3o_tanhf(float y) {
+    if (y != y) return y;
+    const float a = fabsf(y);
+    float r;
+    if (a < 0.5f) {
+        const float z = a * a;
+        float p = -1.4558343870513183e-3f;     /* -929569/638512875 */
+        p = fmaf(p, z, 3.5921280365724811e-3f);  /*  21844/6081075 */
+        p = fmaf(p, z, -8.8632355299021966e-3f); /* -1382/155925 */
+        p = fmaf(p, z, 2.1869488536155203e-2f);  /*  62/2835 */
+        p = fmaf(p, z, -5.3968253968253968e-2f); /* -17/315 */
+        p = fmaf(p, z, 1.3333333333333333e-1f);  /*  2/15 */
+        p = fmaf(p, z, -3.3333333333333333e-1f); /* -1/3 */
+        r = fmaf(a * z, p, a);
+    } else if (a < 9.1f) {
+        const float e = k3o_expf(a + a);
+        r = 1.0f - 2.0f / (e + 1.0f);
+    } else {
+        r = 1.0f;
+    }
+    return copysignf(r, y);
+}
+
+float k3o_sigmoid(float x, int use_libm) {
+    return 1.0f / (1.0f + (use_libm ? expf(-x) : k3o_expf(-x)));
+}
+
+/* ------------------------------------------------------------------------ */
+/* activations                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* SiTU, k3_rocm_ops.cu:66-83: bf16((beta*tanh(g/beta) * sigmoid(g)) *
+ * (lb*tanh(u/lb))), left to right. */
+void k3o_situ(uint16_t *out, const uint16_t *gate, const uint16_t *up,
+              uint64_t n, float beta, float lb, int use_libm) {
+    for (uint64_t i = 0; i < n; i++) {
+        const float g = k3o_bf16_to_f32(gate[i]);
+        const float u = k3o_bf16_to_f32(up[i]);
+        const float tg = use_libm ? tanhf(g / beta) : k3o_tanhf(g / beta);
+        const float tu = use_libm ? tanhf(u / lb) : k3o_tanhf(u / lb);
+        const float bounded_gate = beta * tg;
+        const float sig = k3o_sigmoid(g, use_libm);
+        const float bounded_up = lb * tu;
+        out[i] = k3o_f32_to_bf16((bounded_gate * sig) * bounded_up);
+    }
+}
+
+/* SwiGLU, the beta, lb -> inf limit of SiTU: bf16((g * sigmoid(g)) * u). */
+void k3o_swiglu(uint16_t *out, const uint16_t *gate, const uint16_t *up,
+                uint64_t n, int use_libm) {
+    for (uint64_t i = 0; i < n; i++) {
+        const float g = k3o_bf16_to_f32(gate[i]);
+        const float u = k3o_bf16_to_f32(up[i]);
+        out[i] = k3o_f32_to_bf16((g * k3o_sigmoid(g, use_libm)) * u);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* reductions                                                                */
+/* ------------------------------------------------------------------------ */
+
+/* Wave64 butterfly: stage o replaces lane l by lane[l] + lane[l ^ o] for
+ * o = 32, 16, 8, 4, 2, 1 (what __shfl_xor does); returns lane 0. */
+static float butterfly64(float lane[64]) {
+    float next[64];
+    for (int o = 32; o >= 1; o >>= 1) {
+        for (int l = 0; l < 64; l++) next[l] = lane[l] + lane[l ^ o];
+        memcpy(lane, next, sizeof(next));
+    }
+    return lane[0];
+}
+
+/* LDS tree of the reference kernels: width = n/2 .. 1, p[t] += p[t+width]. */
+static float tree_reduce(float *p, uint32_t n) {
+    for (uint32_t w = n / 2u; w > 0; w /= 2u)
+        for (uint32_t t = 0; t < w; t++) p[t] += p[t + w];
+    return p[0];
+}
+
+/* ---- router logits ------------------------------------------------------ */
+
+/* w64 order: elements in chunks of 8; lane l owns chunks l, l+64, ...;
+ * acc = fmaf(w, x, acc) over each chunk in column order; butterfly64. */
+static float logit_w64(const uint16_t *w, const uint16_t *x, uint32_t h) {
+    float lane[64];
+    const uint32_t chunks = (h + 7u) / 8u;
+    for (uint32_t l = 0; l < 64u; l++) {
+        float acc = 0.0f;
+        for (uint32_t c = l; c < chunks; c += 64u)
+            for (uint32_t i = 8u * c; i < 8u * c + 8u && i < h; i++)
+                acc = fmaf(k3o_bf16_to_f32(w[i]), k3o_bf16_to_f32(x[i]), acc);
+        lane[l] = acc;
+    }
+    return butterfly64(lane);
+}
+
+/* Reference order, k3_rocm_ops.cu:359-425 (quad path): 256 lanes, lane j
+ * sums quads j, j+256, ... as ((p0+p1)+p2)+p3 added to the partial, then the
+ * LDS tree 128 -> 1. The reference is built with -ffast-math, so its own
+ * bits may differ by contraction; this is for tolerance checks only. */
+static float logit_ref256(const uint16_t *w, const uint16_t *x, uint32_t h) {
+    float p[256];
+    for (uint32_t t = 0; t < 256u; t++) {
+        float s = 0.0f;
+        if ((h & 3u) == 0u) {
+            for (uint32_t q = t; q < h / 4u; q += 256u) {
+                const uint32_t i = 4u * q;
+                float a = k3o_bf16_to_f32(w[i]) * k3o_bf16_to_f32(x[i]);
+                a = a + k3o_bf16_to_f32(w[i + 1]) * k3o_bf16_to_f32(x[i + 1]);
+                a = a + k3o_bf16_to_f32(w[i + 2]) * k3o_bf16_to_f32(x[i + 2]);
+                a = a + k3o_bf16_to_f32(w[i + 3]) * k3o_bf16_to_f32(x[i + 3]);
+                s += a;
+            }
+        } else {
+            for (uint32_t i = t; i < h; i += 256u)
+                s += k3o_bf16_to_f32(w[i]) * k3o_bf16_to_f32(x[i]);
+        }
+        p[t] = s;
+    }
+    return tree_reduce(p, 256u);
+}
+
+static float logit_f64(const uint16_t *w, const uint16_t *x, uint32_t h) {
+    double s = 0.0;
+    for (uint32_t i = 0; i < h; i++)
+        s += (double)k3o_bf16_to_f32(w[i]) * (double)k3o_bf16_to_f32(x[i]);
+    return (float)s;
+}
+
+void k3o_router_logits(float *logits, const uint16_t *weights,
+                       const uint16_t *input, uint32_t tokens,
+                       uint32_t experts, uint32_t hidden, int order) {
+    k3o_bf16_gemm_f32(logits, weights, input, tokens, experts, hidden, order);
+}
+
+void k3o_bf16_gemm_f32(float *out, const uint16_t *weights,
+                       const uint16_t *input, uint32_t vectors,
+                       uint32_t rows, uint32_t columns, int order) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t t = 0; t < (int64_t)vectors; t++) {
+        for (int64_t r = 0; r < (int64_t)rows; r++) {
+            const uint16_t *w = weights + (uint64_t)r * columns;
+            const uint16_t *x = input + (uint64_t)t * columns;
+            float v;
+            if (order == 0) v = logit_w64(w, x, columns);
+            else if (order == 1) v = logit_ref256(w, x, columns);
+            else v = logit_f64(w, x, columns);
+            out[(uint64_t)t * rows + r] = v;
+        }
+    }
+}
+
+/* ---- router top-k ------------------------------------------------------- */
+
+/*
+ * k3_rocm_ops.cu:1361-1450 restated as the insertion-sort oracle of
+ * tests/test_k3_moe_smoke.cu:215-253: score = sigmoid(logit); choice =
+ * score + bias; order (choice desc, id asc); weight_r = score_r /
+ * (1e-20 + sum of the k selected scores in rank order) * scale.
+ */
+int k3o_router_topk(uint32_t *ids, float *weights, const float *logits,
+                    const float *bias, uint32_t tokens, uint32_t experts,
+                    uint32_t top_k, float scale, int use_libm) {
+    if (top_k == 0u || top_k > experts || top_k > 64u) return -1;
+    for (uint32_t t = 0; t < tokens; t++) {
+        float choice[64], raw[64];
+        uint32_t id[64];
+        for (uint32_t r = 0; r < top_k; r++) {
+            choice[r] = -INFINITY; raw[r] = 0.0f; id[r] = UINT32_MAX;
+        }
+        const float *lg = logits + (uint64_t)t * experts;
+        for (uint32_t e = 0; e < experts; e++) {
+            const float s = k3o_sigmoid(lg[e], use_libm);
+            const float c = s + bias[e];
+            uint32_t pos = top_k;
+            for (uint32_t r = 0; r < top_k; r++) {
+                if (c > choice[r] || (c == choice[r] && e < id[r])) {
+                    pos = r;
+                    break;
+                }
+            }
+            if (pos == top_k) continue;
+            for (uint32_t r = top_k - 1u; r > pos; r--) {
+                choice[r] = choice[r - 1u]; raw[r] = raw[r - 1u]; id[r] = id[r - 1u];
+            }
+            choice[pos] = c; raw[pos] = s; id[pos] = e;
+        }
+        float denominator = 1e-20f;
+        for (uint32_t r = 0; r < top_k; r++) denominator += raw[r];
+        for (uint32_t r = 0; r < top_k; r++) {
+            ids[(uint64_t)t * top_k + r] = id[r];
+            weights[(uint64_t)t * top_k + r] = raw[r] / denominator * scale;
+        }
+    }
+    return 0;
+}
+
+/* ---- routing plan -------------------------------------------------------- */
+
+/*
+ * Expert-major grouping of k3_engine_prefill.inc:1175-1194: for every
+ * selected expert in ascending id (the physical order of a contiguous
+ * expert store, :1019-1058), rows (token asc, rank asc) with
+ * route = token * top_k + rank. Equivalent to a stable sort of the
+ * flattened routes by expert id.
+ */
+int k3o_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
+                   uint32_t *unique_count, uint32_t *token_index,
+                   uint32_t *route_index, const uint32_t *ids,
+                   uint32_t tokens, uint32_t top_k, uint32_t experts) {
+    const uint64_t routes = (uint64_t)tokens * top_k;
+    memset(counts, 0, sizeof(uint32_t) * experts);
+    for (uint64_t i = 0; i < routes; i++) {
+        if (ids[i] >= experts) return -1;
+        counts[ids[i]]++;
+    }
+    uint32_t running = 0u, u = 0u;
+    for (uint32_t e = 0; e < experts; e++) {
+        offsets[e] = running;
+        running += counts[e];
+        if (counts[e] != 0u) unique[u++] = e;
+    }
+    offsets[experts] = running;
+    *unique_count = u;
+    uint32_t *cursor = (uint32_t *)malloc(sizeof(uint32_t) * experts);
+    if (!cursor) return -2;
+    memcpy(cursor, offsets, sizeof(uint32_t) * experts);
+    for (uint64_t i = 0; i < routes; i++) {
+        const uint32_t e = ids[i];
+        token_index[cursor[e]] = (uint32_t)(i / top_k);
+        route_index[cursor[e]] = (uint32_t)i;
+        cursor[e]++;
+    }
+    free(cursor);
+    return 0;
+}
+
+/* ---- MXFP4 --------------------------------------------------------------- */
+
+static inline float nib(const uint8_t *packed_row, uint32_t col) {
+    const uint8_t b = packed_row[col / 2u];
+    return k3o_e2m1((col & 1u) ? (uint8_t)(b >> 4) : (uint8_t)(b & 15u));
+}
+
+/* w64 order: lane l owns 32-column groups l, l+64, ...; per group
+ * gs = fmaf(e2m1, x, gs) over its 32 columns in order, then
+ * acc = fmaf(gs, e8m0, acc); butterfly64. */
+static float mx_row_w64(const uint8_t *p, const uint8_t *s,
+                        const uint16_t *x, uint32_t cols) {
+    float lane[64];
+    const uint32_t groups = cols / 32u;
+    for (uint32_t l = 0; l < 64u; l++) {
+        float acc = 0.0f;
+        for (uint32_t g = l; g < groups; g += 64u) {
+            float gs = 0.0f;
+            for (uint32_t c = 32u * g; c < 32u * g + 32u; c++)
+                gs = fmaf(nib(p, c), k3o_bf16_to_f32(x[c]), gs);
+            acc = fmaf(gs, k3o_e8m0(s[g]), acc);
+        }
+        lane[l] = acc;
+    }
+    return butterfly64(lane);
+}
+
+/* Reference order, k3_rocm_ops.cu:225-273: 128 lanes, lane j owns groups
+ * j, j+128, ...; partial += dot8(x)+dot8(y)+dot8(z)+dot8(w) where each dot8
+ * sums e2m1*scale*x over 8 columns; LDS tree 64 -> 1. */
+static float mx_row_ref128(const uint8_t *p, const uint8_t *s,
+                           const uint16_t *x, uint32_t cols) {
+    float part[128];
+    const uint32_t groups = cols / 32u;
+    for (uint32_t t = 0; t < 128u; t++) {
+        float acc = 0.0f;
+        for (uint32_t g = t; g < groups; g += 128u) {
+            const float sc = k3o_e8m0(s[g]);
+            float d[4];
+            for (uint32_t q = 0; q < 4u; q++) {
+                float pd = 0.0f;
+                for (uint32_t i = 0; i < 8u; i++) {
+                    const uint32_t c = 32u * g + 8u * q + i;
+                    pd += nib(p, c) * sc * k3o_bf16_to_f32(x[c]);
+                }
+                d[q] = pd;
+            }
+            acc += ((d[0] + d[1]) + d[2]) + d[3];
+        }
+        part[t] = acc;
+    }
+    return tree_reduce(part, 128u);
+}
+
+static double mx_row_f64(const uint8_t *p, const uint8_t *s,
+                         const uint16_t *x, uint32_t cols) {
+    double acc = 0.0;
+    for (uint32_t c = 0; c < cols; c++)
+        acc += (double)nib(p, c) * (double)k3o_e8m0(s[c / 32u]) *
+               (double)k3o_bf16_to_f32(x[c]);
+    return acc;
+}
+
+void k3o_mxfp4_gemm(uint16_t *out, float *out_f32, const uint8_t *packed,
+                    const uint8_t *scales, const uint16_t *input,
+                    uint32_t vectors, uint32_t rows, uint32_t columns,
+                    int order) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t t = 0; t < (int64_t)vectors; t++) {
+        for (int64_t r = 0; r < (int64_t)rows; r++) {
+            const uint8_t *p = packed + (uint64_t)r * (columns / 2u);
+            const uint8_t *s = scales + (uint64_t)r * (columns / 32u);
+            const uint16_t *x = input + (uint64_t)t * columns;
+            float v;
+            if (order == 0) v = mx_row_w64(p, s, x, columns);
+            else if (order == 1) v = mx_row_ref128(p, s, x, columns);
+            else v = (float)mx_row_f64(p, s, x, columns);
+            const uint64_t o = (uint64_t)t * rows + r;
+            if (out) out[o] = k3o_f32_to_bf16(v);
+            if (out_f32) out_f32[o] = v;
+        }
+    }
+}
+
+/* ---- combine ------------------------------------------------------------- */
+
+/* k3_rocm_ops.cu:1452-1474: sum starts at 0 and adds w[r] * y[r] in rank
+ * order, product and sum each rounded to fp32 (as the source is written). */
+void k3o_weighted_sum(uint16_t *out, const uint16_t *vectors,
+                      const float *weights, uint32_t tokens,
+                      uint32_t vector_count, uint32_t hidden) {
+    for (uint32_t t = 0; t < tokens; t++) {
+        const uint16_t *v = vectors + (uint64_t)t * vector_count * hidden;
+        const float *w = weights + (uint64_t)t * vector_count;
+        for (uint32_t d = 0; d < hidden; d++) {
+            float sum = 0.0f;
+            for (uint32_t r = 0; r < vector_count; r++) {
+                const float prod = w[r] * k3o_bf16_to_f32(v[(uint64_t)r * hidden + d]);
+                sum = sum + prod;
+            }
+            out[(uint64_t)t * hidden + d] = k3o_f32_to_bf16(sum);
+        }
+    }
+}
+
+/* k3_rocm_ops.cu:1499-1510. */
+void k3o_add(uint16_t *out, const uint16_t *left, const uint16_t *right,
+             uint64_t n) {
+    for (uint64_t i = 0; i < n; i++)
+        out[i] = k3o_f32_to_bf16(k3o_bf16_to_f32(left[i]) + k3o_bf16_to_f32(right[i]));
+}
+
+/* k3_rocm_ops.cu:1476-1497: gather out[i] = in[ids[i]]; scatter
+ * out[ids[i]] = in[i]. */
+void k3o_copy_rows(uint16_t *out, const uint16_t *in, const uint32_t *row_ids,
+                   uint32_t row_count, uint32_t row_size, int scatter) {
+    for (uint32_t i = 0; i < row_count; i++) {
+        const uint64_t a = (uint64_t)i * row_size;
+        const uint64_t b = (uint64_t)row_ids[i] * row_size;
+        if (scatter) memcpy(out + b, in + a, (size_t)row_size * 2u);
+        else memcpy(out + a, in + b, (size_t)row_size * 2u);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* whole layer                                                               */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Per token t (config form, or K3-native expert stage when hidden = latent):
+ *   logits = router(x_t)                      k3_engine.cu:1554-1557
+ *   ids, w = topk(logits, bias, k, scale)     k3_engine.cu:1558-1563
+ *   for rank r: e = ids[r]                    k3_engine.cu:1032-1066
+ *     g = bf16(W1_e x), u = bf16(W3_e x), a = act(g, u), y_r = bf16(W2_e a)
+ *   c = bf16(sum_r w_r y_r)                   k3_engine.cu:1851-1855
+ *   out = bf16(residual + c)                  k3_engine.cu:1889-1897
+ * (the K3-native RMSNorm / routed-up / shared-expert tail is not part of
+ * this function).
+ */
+int k3o_layer(const k3o_shape *sh, uint32_t tokens,
+              const uint16_t *hidden_in, const uint16_t *residual,
+              const uint16_t *router_weight, const float *router_bias,
+              const k3o_expert *experts,
+              const uint32_t *ids_in, const float *weights_in,
+              const uint32_t *token_list, uint32_t token_list_count,
+              uint16_t *output, uint32_t *ids_out, float *weights_out,
+              float *logits_out, uint16_t *expert_out, int gemv_order,
+              int threads) {
+    const uint32_t H = sh->hidden, E = sh->experts, K = sh->top_k, F = sh->ffn;
+    const uint32_t n = token_list ? token_list_count : tokens;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#else
+    (void)threads;
+#endif
+    int status = 0;
+    float *logits = (float *)malloc(sizeof(float) * (uint64_t)E * (n ? n : 1));
+    uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * (uint64_t)K * (n ? n : 1));
+    float *wts = (float *)malloc(sizeof(float) * (uint64_t)K * (n ? n : 1));
+    uint16_t *ys = (uint16_t *)malloc(sizeof(uint16_t) * (uint64_t)K * H * (n ? n : 1));
+    if (!logits || !ids || !wts || !ys) { status = -2; goto done; }
+
+    for (uint32_t i = 0; i < n; i++) {
+        const uint32_t t = token_list ? token_list[i] : i;
+        const uint16_t *x = hidden_in + (uint64_t)t * H;
+        if (ids_in) {
+            memcpy(ids + (uint64_t)i * K, ids_in + (uint64_t)t * K, 4u * K);
+            memcpy(wts + (uint64_t)i * K, weights_in + (uint64_t)t * K, 4u * K);
+        } else {
+            k3o_bf16_gemm_f32(logits + (uint64_t)i * E, router_weight, x, 1u, E, H,
+                              gemv_order == 1 ? 1 : 0);
+            k3o_router_topk(ids + (uint64_t)i * K, wts + (uint64_t)i * K,
+                            logits + (uint64_t)i * E, router_bias, 1u, E, K,
+                            sh->scale, 0);
+        }
+        for (uint32_t r = 0; r < K; r++) {
+            const uint32_t e = ids[(uint64_t)i * K + r];
+            if (e >= E || !experts[e].w1_packed) { status = -1; goto done; }
+        }
+    }
+
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t job = 0; job < (int64_t)n * K; job++) {
+        const uint32_t i = (uint32_t)(job / K), r = (uint32_t)(job % K);
+        const uint32_t t = token_list ? token_list[i] : i;
+        const uint16_t *x = hidden_in + (uint64_t)t * H;
+        const k3o_expert *ex = &experts[ids[(uint64_t)i * K + r]];
+        uint16_t *g = (uint16_t *)malloc(2u * F), *u = (uint16_t *)malloc(2u * F);
+        uint16_t *a = (uint16_t *)malloc(2u * F);
+        const int ord = gemv_order;
+        for (uint32_t row = 0; row < F; row++) {
+            const uint64_t po = (uint64_t)row * (H / 2u), so = (uint64_t)row * (H / 32u);
+            float vg, vu;
+            if (ord == 0) {
+                vg = mx_row_w64(ex->w1_packed + po, ex->w1_scales + so, x, H);
+                vu = mx_row_w64(ex->w3_packed + po, ex->w3_scales + so, x, H);
+            } else if (ord == 1) {
+                vg = mx_row_ref128(ex->w1_packed + po, ex->w1_scales + so, x, H);
+                vu = mx_row_ref128(ex->w3_packed + po, ex->w3_scales + so, x, H);
+            } else {
+                vg = (float)mx_row_f64(ex->w1_packed + po, ex->w1_scales + so, x, H);
+                vu = (float)mx_row_f64(ex->w3_packed + po, ex->w3_scales + so, x, H);
+            }
+            g[row] = k3o_f32_to_bf16(vg);
+            u[row] = k3o_f32_to_bf16(vu);
+        }
+        if (sh->activation == 1u) k3o_swiglu(a, g, u, F, 0);
+        else k3o_situ(a, g, u, F, sh->beta, sh->linear_beta, 0);
+        uint16_t *y = ys + ((uint64_t)i * K + r) * H;
+        for (uint32_t row = 0; row < H; row++) {
+            const uint64_t po = (uint64_t)row * (F / 2u), so = (uint64_t)row * (F / 32u);
+            float v;
+            if (ord == 0) v = mx_row_w64(ex->w2_packed + po, ex->w2_scales + so, a, F);
+            else if (ord == 1) v = mx_row_ref128(ex->w2_packed + po, ex->w2_scales + so, a, F);
+            else v = (float)mx_row_f64(ex->w2_packed + po, ex->w2_scales + so, a, F);
+            y[row] = k3o_f32_to_bf16(v);
+        }
+        free(g); free(u); free(a);
+    }
+
+    for (uint32_t i = 0; i < n; i++) {
+        const uint32_t t = token_list ? token_list[i] : i;
+        uint16_t *c = (uint16_t *)malloc(2u * H);
+        k3o_weighted_sum(c, ys + (uint64_t)i * K * H, wts + (uint64_t)i * K, 1u, K, H);
+        if (residual) k3o_add(output + (uint64_t)i * H, residual + (uint64_t)t * H, c, H);
+        else memcpy(output + (uint64_t)i * H, c, 2u * H);
+        free(c);
+        if (ids_out) memcpy(ids_out + (uint64_t)i * K, ids + (uint64_t)i * K, 4u * K);
+        if (weights_out) memcpy(weights_out + (uint64_t)i * K, wts + (uint64_t)i * K, 4u * K);
+        if (logits_out && !ids_in) memcpy(logits_out + (uint64_t)i * E, logits + (uint64_t)i * E, 4u * E);
+        if (expert_out) memcpy(expert_out + (uint64_t)i * K * H, ys + (uint64_t)i * K * H, 2u * K * H);
+    }
+done:
+    free(logits); free(ids); free(wts); free(ys);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
+/* prefill workspace ledger                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* k3_prefill.c:136-234 per-token byte counts for the K3 shape
+ * (hidden 7168, KDA inner 12288, head dim 128, dense 33792, latent 3584,
+ * expert hidden 3072, shared 6144, top-k 16, 896 experts, 96 heads, MLA
+ * q-lora 1536, q 96*192, cache dim 576, 24 MLA layers). */
+int k3o_prefill_workspace(uint32_t chunk, k3o_workspace *o) {
+    const uint64_t b = 2u;
+    const uint64_t hidden = 7168u * b, inner = 12288u * b, dense = 33792u * b;
+    const uint64_t main_t = 5u * hidden + 10u * inner + 128u * b + 96u * b + 3u * dense;
+    const uint64_t hid_t = 2u * hidden, attn_t = 8u * hidden;
+    const uint64_t moe_t = 896u * 4u +
+        (3584u + 3u * 3072u + 16u * 3584u + 2u * 3584u + 7168u + 3u * 6144u + 7168u) * b;
+    const uint64_t mla_t = (2u * 1536u + 96u * 192u + 576u + 96u * 576u + 3u * 12288u) * b;
+    const uint64_t route_t = 16u * 8u, index_t = 8u;
+    o->hidden_row_bytes = hid_t * chunk;
+    o->attn_res_row_bytes = attn_t * chunk;
+    o->main_scratch_bytes = main_t * chunk;
+    o->moe_scratch_bytes = moe_t * chunk;
+    o->mla_scratch_bytes = mla_t * chunk;
+    o->route_bytes = route_t * chunk;
+    o->expert_index_bytes = index_t * chunk;
+    o->batch_workspace_bytes = o->hidden_row_bytes + o->attn_res_row_bytes +
+        o->main_scratch_bytes + o->moe_scratch_bytes + o->mla_scratch_bytes +
+        o->route_bytes + o->expert_index_bytes;
+    const uint64_t one = hid_t + attn_t + main_t + moe_t + mla_t + route_t + index_t;
+    o->incremental_workspace_bytes =
+        o->batch_workspace_bytes > one ? o->batch_workspace_bytes - one : 0u;
+    o->mla_append_bytes = (uint64_t)chunk * 24u * 576u * b;
+    return 0;
+}

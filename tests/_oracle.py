@@ -1,0 +1,181 @@
+"""ctypes bridge to oracle/libk3moe_oracle.so (the CPU checker).
+
+Test infrastructure only: the product never imports this module.
+"""
+import ctypes
+import pathlib
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+ORACLE = ROOT / "oracle" / "libk3moe_oracle.so"
+REF_OPS = ROOT / "oracle" / "_ref" / "libk3ref_ops.so"
+REF_PREFILL = ROOT / "oracle" / "_ref" / "libk3ref_prefill.so"
+
+ORDER_W64, ORDER_REF, ORDER_F64 = 0, 1, 2
+
+_p = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_f = ctypes.c_float
+_i = ctypes.c_int
+
+
+class Expert(ctypes.Structure):
+    _fields_ = [(n, _p) for n in ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")]
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [("hidden", _u32), ("experts", _u32), ("top_k", _u32), ("ffn", _u32),
+                ("scale", _f), ("activation", _u32), ("beta", _f), ("linear_beta", _f)]
+
+
+class Workspace(ctypes.Structure):
+    _fields_ = [(n, _u64) for n in (
+        "hidden_row_bytes", "attn_res_row_bytes", "main_scratch_bytes", "moe_scratch_bytes",
+        "mla_scratch_bytes", "route_bytes", "expert_index_bytes", "batch_workspace_bytes",
+        "incremental_workspace_bytes", "mla_append_bytes")]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not ORACLE.exists():
+            raise RuntimeError(f"{ORACLE} not built (make -C oracle)")
+        L = ctypes.CDLL(str(ORACLE))
+        sig = {
+            "k3o_bf16_to_f32": (_f, [ctypes.c_uint16]),
+            "k3o_f32_to_bf16": (ctypes.c_uint16, [_f]),
+            "k3o_e2m1": (_f, [ctypes.c_uint8]),
+            "k3o_e8m0": (_f, [ctypes.c_uint8]),
+            "k3o_expf": (_f, [_f]),
+            "k3o_tanhf": (_f, [_f]),
+            "k3o_sigmoid": (_f, [_f, _i]),
+            "k3o_situ": (None, [_p, _p, _p, _u64, _f, _f, _i]),
+            "k3o_swiglu": (None, [_p, _p, _p, _u64, _i]),
+            "k3o_router_logits": (None, [_p, _p, _p, _u32, _u32, _u32, _i]),
+            "k3o_router_topk": (_i, [_p, _p, _p, _p, _u32, _u32, _u32, _f, _i]),
+            "k3o_route_plan": (_i, [_p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32]),
+            "k3o_mxfp4_gemm": (None, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _i]),
+            "k3o_bf16_gemm_f32": (None, [_p, _p, _p, _u32, _u32, _u32, _i]),
+            "k3o_weighted_sum": (None, [_p, _p, _p, _u32, _u32, _u32]),
+            "k3o_add": (None, [_p, _p, _p, _u64]),
+            "k3o_copy_rows": (None, [_p, _p, _p, _u32, _u32, _i]),
+            "k3o_layer": (_i, [ctypes.POINTER(Shape), _u32, _p, _p, _p, _p, ctypes.POINTER(Expert),
+                              _p, _p, _p, _u32, _p, _p, _p, _p, _p, _i, _i]),
+            "k3o_prefill_workspace": (_i, [_u32, ctypes.POINTER(Workspace)]),
+        }
+        for n, (r, a) in sig.items():
+            fn = getattr(L, n)
+            fn.restype, fn.argtypes = r, a
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_p)
+
+
+def router_logits(w, x, order=ORDER_W64):
+    E, H = w.shape
+    T = x.shape[0]
+    out = np.empty((T, E), np.float32)
+    lib().k3o_router_logits(_ptr(out), _ptr(w), _ptr(x), T, E, H, order)
+    return out
+
+
+def router_topk(logits, bias, k, scale, use_libm=False):
+    T, E = logits.shape
+    ids = np.empty((T, k), np.uint32)
+    w = np.empty((T, k), np.float32)
+    assert lib().k3o_router_topk(_ptr(ids), _ptr(w), _ptr(np.ascontiguousarray(logits)),
+                                 _ptr(bias), T, E, k, scale, int(use_libm)) == 0
+    return ids, w
+
+
+def route_plan(ids, experts):
+    T, k = ids.shape
+    counts = np.empty(experts, np.uint32)
+    offsets = np.empty(experts + 1, np.uint32)
+    unique = np.zeros(experts, np.uint32)
+    ucount = np.zeros(1, np.uint32)
+    tok = np.empty(T * k, np.uint32)
+    route = np.empty(T * k, np.uint32)
+    assert lib().k3o_route_plan(_ptr(counts), _ptr(offsets), _ptr(unique), _ptr(ucount),
+                                _ptr(tok), _ptr(route), _ptr(np.ascontiguousarray(ids)), T, k,
+                                experts) == 0
+    return counts, offsets, unique[:ucount[0]], tok, route
+
+
+def mxfp4_gemm(packed, scales, x, rows, cols, order=ORDER_W64):
+    T = x.shape[0]
+    out = np.empty((T, rows), np.uint16)
+    f = np.empty((T, rows), np.float32)
+    lib().k3o_mxfp4_gemm(_ptr(out), _ptr(f), _ptr(packed), _ptr(scales), _ptr(x), T, rows, cols,
+                         order)
+    return out, f
+
+
+def bf16_gemm_f32(w, x, order=ORDER_W64):
+    rows, cols = w.shape
+    T = x.shape[0]
+    out = np.empty((T, rows), np.float32)
+    lib().k3o_bf16_gemm_f32(_ptr(out), _ptr(w), _ptr(x), T, rows, cols, order)
+    return out
+
+
+def situ(g, u, beta=4.0, lb=25.0, use_libm=False):
+    out = np.empty_like(g)
+    lib().k3o_situ(_ptr(out), _ptr(g), _ptr(u), g.size, beta, lb, int(use_libm))
+    return out
+
+
+def swiglu(g, u, use_libm=False):
+    out = np.empty_like(g)
+    lib().k3o_swiglu(_ptr(out), _ptr(g), _ptr(u), g.size, int(use_libm))
+    return out
+
+
+def weighted_sum(v, w):
+    T, K, H = v.shape
+    out = np.empty((T, H), np.uint16)
+    lib().k3o_weighted_sum(_ptr(out), _ptr(v), _ptr(w), T, K, H)
+    return out
+
+
+def add(a, b):
+    out = np.empty_like(a)
+    lib().k3o_add(_ptr(out), _ptr(a), _ptr(b), a.size)
+    return out
+
+
+def layer(cfg, inputs, experts, tokens=None, ids=None, weights=None, order=ORDER_W64,
+          threads=0):
+    """experts: dict e -> list of six uint8 arrays (w1p, w1s, w2p, w2s, w3p, w3s)."""
+    T = inputs.hidden.shape[0]
+    shape = Shape(cfg.hidden, cfg.experts, cfg.top_k, cfg.ffn, cfg.scale, cfg.activation,
+                  cfg.beta, cfg.linear_beta)
+    table = (Expert * cfg.experts)()
+    keep = []
+    for e, tensors in experts.items():
+        arrs = [np.ascontiguousarray(t) for t in tensors]
+        keep.append(arrs)
+        table[e] = Expert(*[a.ctypes.data for a in arrs])
+    tl = None if tokens is None else np.ascontiguousarray(tokens, dtype=np.uint32)
+    n = T if tl is None else tl.size
+    out = np.empty((n, cfg.hidden), np.uint16)
+    ids_out = np.empty((n, cfg.top_k), np.uint32)
+    w_out = np.empty((n, cfg.top_k), np.float32)
+    logits = np.empty((n, cfg.experts), np.float32)
+    yout = np.empty((n, cfg.top_k, cfg.hidden), np.uint16)
+    rc = lib().k3o_layer(ctypes.byref(shape), T, _ptr(inputs.hidden), _ptr(inputs.residual),
+                         _ptr(inputs.router_weight), _ptr(inputs.router_bias), table,
+                         _ptr(ids), _ptr(weights), _ptr(tl), 0 if tl is None else tl.size,
+                         _ptr(out), _ptr(ids_out), _ptr(w_out), _ptr(logits), _ptr(yout), order,
+                         threads)
+    if rc != 0:
+        raise RuntimeError(f"k3o_layer failed ({rc})")
+    return dict(output=out, ids=ids_out, weights=w_out, logits=logits, expert_out=yout)

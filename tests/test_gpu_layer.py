@@ -1,0 +1,160 @@
+"""GPU parity of the fused routed-MoE layer (k3_moe_forward_bf16) against the
+CPU oracle on the seeded benchmark configurations.
+
+Exact precision is bit-identical to the oracle's w64 order: logits, expert
+ids, route weights, the routing plan and the layer output.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from moonshine_amd import layer as L
+from moonshine_amd._lib import lib
+from moonshine_amd.synth import CONFIGS, K3_NATIVE, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+_stores = {}
+
+
+def get_layer(cfg, inputs, cuda):
+    key = (cfg.experts, cfg.hidden, cfg.ffn, cfg.seed)
+    if key not in _stores:
+        _stores.clear()
+        torch.cuda.empty_cache()
+        _stores[key] = L.ExpertStore(cfg.experts, cfg.hidden, cfg.ffn, seed=cfg.seed, device=cuda)
+    return L.build_layer(cfg, inputs, device=cuda, store=_stores[key])
+
+
+def run(cfg, inputs, moe, cuda):
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    T, k = x.shape[0], cfg.top_k
+    ids = torch.zeros((T, k), dtype=torch.int32, device=cuda)
+    w = torch.zeros((T, k), dtype=torch.float32, device=cuda)
+    out = moe.forward(x, r, ids=ids, weights=w)
+    torch.cuda.synchronize()
+    return (L.bf16_bits(out), ids.cpu().numpy().view(np.uint32), w.cpu().numpy())
+
+
+def host_experts(store, ids):
+    return {int(e): store.host_expert(int(e)) for e in np.unique(ids)}
+
+
+def check_tokens(cfg, inputs, store, got_out, got_ids, got_w, tokens):
+    tokens = np.asarray(tokens, dtype=np.uint32)
+    want = O.layer(cfg, inputs, host_experts(store, got_ids[tokens]), tokens=tokens)
+    np.testing.assert_array_equal(got_ids[tokens], want["ids"])
+    np.testing.assert_array_equal(got_w[tokens], want["weights"])
+    np.testing.assert_array_equal(got_out[tokens], want["output"])
+
+
+def test_synth_store_host_matches_device(cuda):
+    cfg = CONFIGS[0]
+    store = L.ExpertStore(cfg.experts, cfg.hidden, cfg.ffn, seed=cfg.seed, device=cuda)
+    for e in (0, 17, cfg.experts - 1):
+        for d, h in zip(store.device_expert(e), store.host_expert(e)):
+            np.testing.assert_array_equal(d.cpu().numpy(), h)
+    s = store.host_expert(3)[1]
+    assert s.min() >= 121 and s.max() <= 125
+
+
+@pytest.mark.parametrize("cfg", [CONFIGS[0], CONFIGS[1], K3_NATIVE], ids=lambda c: c.name)
+def test_decode_layer_bitexact(cuda, cfg):
+    inputs = make_inputs(cfg)
+    moe = get_layer(cfg, inputs, cuda)
+    out, ids, w = run(cfg, inputs, moe, cuda)
+    want = O.layer(cfg, inputs, host_experts(moe.store, ids))
+    # logits bit-exact too (fixed w64 order)
+    logits = torch.zeros((1, cfg.experts), dtype=torch.float32, device=cuda)
+    from moonshine_amd import ops
+    assert ops.k3_rocm_bf16_gemv_f32(logits, moe.router_weight, L.bf16_tensor(inputs.hidden, cuda),
+                                     cfg.experts, cfg.hidden)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(logits.cpu().numpy(), want["logits"])
+    np.testing.assert_array_equal(ids, want["ids"])
+    np.testing.assert_array_equal(w, want["weights"])
+    np.testing.assert_array_equal(out, want["output"])
+    assert len(set(ids[0].tolist())) == cfg.top_k
+    np.testing.assert_allclose(w.sum(), cfg.scale, rtol=1e-6)
+
+
+@pytest.mark.parametrize("cfg_index,check", [(0, None), (2, 12), (3, 6)])
+def test_batched_layer_bitexact(cuda, cfg_index, check):
+    cfg = CONFIGS[cfg_index]
+    T = cfg.tokens if cfg_index else 40
+    inputs = make_inputs(cfg, tokens=T)
+    moe = get_layer(cfg, inputs, cuda)
+    out, ids, w = run(cfg, inputs, moe, cuda)
+    # routing of every token is checked against the oracle router
+    want_logits = O.router_logits(inputs.router_weight, inputs.hidden)
+    want_ids, want_w = O.router_topk(want_logits, inputs.router_bias, cfg.top_k, cfg.scale)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(w, want_w)
+    rng = np.random.default_rng(5)
+    tokens = np.arange(T) if check is None else np.sort(rng.choice(T, check, replace=False))
+    check_tokens(cfg, inputs, moe.store, out, ids, w, tokens)
+    # a token alone (decode path) gives the same bits as inside the batch
+    t = int(tokens[-1])
+    one = make_inputs(cfg, tokens=T)
+    one.hidden, one.residual = one.hidden[t:t + 1].copy(), one.residual[t:t + 1].copy()
+    o1, i1, w1 = run(cfg, one, moe, cuda)
+    np.testing.assert_array_equal(i1[0], ids[t])
+    np.testing.assert_array_equal(o1[0], out[t])
+
+
+def test_expert_stage_on_given_routes(cuda):
+    cfg = CONFIGS[0]
+    T = 9
+    inputs = make_inputs(cfg, tokens=T)
+    moe = get_layer(cfg, inputs, cuda)
+    rng = np.random.default_rng(9)
+    ids = np.stack([rng.choice(cfg.experts, cfg.top_k, replace=False) for _ in range(T)]).astype(np.uint32)
+    ids[3] = [5, 5, 6, 7]  # duplicate route within a token: second one dropped
+    w = rng.random((T, cfg.top_k)).astype(np.float32)
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    out = moe.experts_only(x, torch.from_numpy(ids.view(np.int32)).to(cuda), torch.from_numpy(w).to(cuda), r)
+    torch.cuda.synchronize()
+    got = L.bf16_bits(out)
+    keep = np.array([0, 1, 2, 4, 5, 6, 7, 8])
+    want = O.layer(cfg, inputs, host_experts(moe.store, ids), ids=ids, weights=w, tokens=keep)
+    np.testing.assert_array_equal(got[keep], want["output"])
+
+
+@pytest.mark.parametrize("T,E,k,zipf", [(1, 896, 16, False), (300, 64, 4, False), (8192, 896, 16, True),
+                                        (777, 1024, 32, False)])
+def test_route_plan_bitexact(cuda, T, E, k, zipf):
+    rng = np.random.default_rng(T + E)
+    if zipf:
+        p = (np.arange(1, E + 1) ** -1.1)
+        p /= p.sum()
+        ids = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.uint32)
+    else:
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.uint32)
+    d_ids = torch.from_numpy(ids.view(np.int32)).to(cuda)
+    counts = torch.zeros(E, dtype=torch.int32, device=cuda)
+    offsets = torch.zeros(E + 1, dtype=torch.int32, device=cuda)
+    unique = torch.zeros(E, dtype=torch.int32, device=cuda)
+    summary = torch.zeros(4, dtype=torch.int32, device=cuda)
+    tok = torch.zeros(T * k, dtype=torch.int32, device=cuda)
+    route = torch.zeros(T * k, dtype=torch.int32, device=cuda)
+    nscratch = lib().k3_moe_plan_scratch_bytes(T, E)
+    scratch = torch.zeros(nscratch, dtype=torch.uint8, device=cuda)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert lib().k3_moe_route_plan(P(counts), P(offsets), P(unique), P(summary), P(tok), P(route),
+                                   P(d_ids), T, k, E, P(scratch), nscratch,
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    c, o, u, t_i, r_i = O.route_plan(ids, E)
+    h = lambda t: t.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(h(counts), c)
+    np.testing.assert_array_equal(h(offsets), o)
+    s = h(summary)
+    assert s[0] == u.size and s[1] == 0 and s[2] == c.max()
+    np.testing.assert_array_equal(h(unique)[:u.size], u)
+    np.testing.assert_array_equal(h(tok), t_i)
+    np.testing.assert_array_equal(h(route), r_i)

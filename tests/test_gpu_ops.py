@@ -1,0 +1,249 @@
+"""GPU parity of the k3_rocm_ops.h entry points against the CPU oracle.
+
+The w64-order kernels must match the oracle bit for bit; the reference
+built from its own sources (oracle/_ref, when present) is compared within
+the reference's own test tolerances.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from moonshine_amd import ops
+from moonshine_amd.synth import bf16_bits_to_f32, f32_to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def rand_bf16(rng, shape, scale=1.0):
+    return f32_to_bf16_bits(rng.normal(0, scale, shape).astype(np.float32))
+
+
+def rand_mx(rng, rows, cols, lo=121, hi=125):
+    packed = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    scales = rng.integers(lo, hi + 1, (rows, cols // 32), dtype=np.uint8)
+    return packed, scales
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows,cols", [(128, 512), (96, 7168), (64, 2048), (40, 3584), (7, 3072)])
+def test_mxfp4_gemv_bitexact(cuda, rows, cols):
+    rng = np.random.default_rng(rows * 31 + cols)
+    p, s = rand_mx(rng, rows, cols)
+    x = rand_bf16(rng, (1, cols))
+    out = torch.zeros(rows, dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_mxfp4_gemv_bf16(out, dev(p, cuda), dev(s, cuda), dev(x.view(np.int16), cuda),
+                                       rows, cols)
+    sync()
+    want, _ = O.mxfp4_gemm(p, s, x, rows, cols)
+    np.testing.assert_array_equal(host(out).view(np.uint16), want[0])
+
+
+def test_e2m1_nibble_order(cuda):
+    """Single-nonzero KAT: code c at column j, x = 1 at j only -> e2m1(c)*2^(s-127)."""
+    rows, cols = 16, 64
+    p = np.zeros((rows, cols // 2), np.uint8)
+    s = np.full((rows, cols // 32), 127, np.uint8)
+    for r in range(rows):
+        col = (r * 5) % cols
+        code = r  # all 16 codes
+        p[r, col // 2] = code << 4 if col & 1 else code
+        s[r, col // 32] = 120 + r % 8
+    outs = []
+    for j in range(cols):
+        x = np.zeros((1, cols), np.uint16)
+        x[0, j] = 0x3F80  # 1.0
+        outs.append(x)
+    x = np.concatenate(outs)  # [64, cols]
+    out = torch.zeros((cols, rows), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_mxfp4_gemm_bf16(out, dev(p, cuda), dev(s, cuda), dev(x.view(np.int16), cuda),
+                                       cols, rows, cols)
+    sync()
+    got = bf16_bits_to_f32(host(out).view(np.uint16))
+    table = [0, .5, 1, 1.5, 2, 3, 4, 6]
+    for r in range(rows):
+        col = (r * 5) % cols
+        v = table[r & 7] * (-1 if r & 8 else 1) * 2.0 ** (120 + r % 8 - 127)
+        for j in range(cols):
+            assert got[j, r] == (v if j == col else 0.0), (r, j)
+
+
+@pytest.mark.parametrize("T", [2, 5, 16, 33, 64])
+def test_mxfp4_gemm_batch_equals_sequential_and_tiles(cuda, T):
+    rows, cols = 64, 3584
+    rng = np.random.default_rng(T)
+    p, s = rand_mx(rng, rows, cols)
+    x = rand_bf16(rng, (T, cols))
+    dp, ds, dx = dev(p, cuda), dev(s, cuda), dev(x.view(np.int16), cuda)
+    ref = torch.zeros((T, rows), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_mxfp4_gemm_bf16(ref, dp, ds, dx, T, rows, cols)
+    for tile in (16, 32, 64):
+        o = torch.zeros_like(ref)
+        assert ops.k3_rocm_mxfp4_gemm_tiled_bf16(o, dp, ds, dx, T, rows, cols, tile)
+        sync()
+        assert torch.equal(o, ref), tile
+    assert not ops.k3_rocm_mxfp4_gemm_tiled_bf16(ref, dp, ds, dx, T, rows, cols, 8)
+    for t in range(T):
+        o = torch.zeros(rows, dtype=torch.int16, device=cuda)
+        assert ops.k3_rocm_mxfp4_gemv_bf16(o, dp, ds, dx[t], rows, cols)
+        sync()
+        assert torch.equal(o, ref[t]), t
+    want, _ = O.mxfp4_gemm(p, s, x, rows, cols)
+    np.testing.assert_array_equal(host(ref).view(np.uint16), want)
+
+
+def test_mxfp4_misaligned_8mod16(cuda):
+    """Tensors starting at 8 mod 16 (k3_rocm_ops.cu:207-223) give the same bits."""
+    rows, cols = 32, 1024
+    rng = np.random.default_rng(7)
+    p, s = rand_mx(rng, rows, cols)
+    x = rand_bf16(rng, (1, cols))
+    buf = torch.zeros(p.size + 8, dtype=torch.uint8, device=cuda)
+    buf[8:] = dev(p.reshape(-1), cuda)
+    out = torch.zeros(rows, dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_mxfp4_gemv_bf16(out, buf[8:], dev(s, cuda), dev(x.view(np.int16), cuda),
+                                       rows, cols)
+    sync()
+    want, _ = O.mxfp4_gemm(p, s, x, rows, cols)
+    np.testing.assert_array_equal(host(out).view(np.uint16), want[0])
+
+
+@pytest.mark.parametrize("T,E,H", [(1, 896, 7168), (3, 64, 2048), (17, 896, 7168), (4, 100, 1001)])
+def test_router_logits_bitexact(cuda, T, E, H):
+    rng = np.random.default_rng(E + H + T)
+    w = rand_bf16(rng, (E, H), 0.02)
+    x = rand_bf16(rng, (T, H))
+    out = torch.zeros((T, E), dtype=torch.float32, device=cuda)
+    assert ops.k3_rocm_bf16_gemm_f32(out, dev(w.view(np.int16), cuda), dev(x.view(np.int16), cuda),
+                                     T, E, H)
+    sync()
+    want = O.router_logits(w, x)
+    np.testing.assert_array_equal(host(out), want)
+    if T > 1:
+        for tile in (16, 32, 64):
+            o2 = torch.zeros_like(out)
+            assert ops.k3_rocm_bf16_gemm_tiled_f32(o2, dev(w.view(np.int16), cuda),
+                                                   dev(x.view(np.int16), cuda), T, E, H, tile)
+            sync()
+            assert torch.equal(o2, out)
+
+
+@pytest.mark.parametrize("E,k,scale", [(896, 16, 2.5), (64, 4, 1.0), (1000, 32, 1.0), (16, 16, 2.5)])
+def test_router_topk_bitexact(cuda, E, k, scale):
+    rng = np.random.default_rng(E * k)
+    T = 37
+    logits = rng.normal(0, 1.7, (T, E)).astype(np.float32)
+    logits[0, :] = 0.25  # all-equal scores: ties broken by lower id
+    logits[1, ::3] = logits[1, 0]  # many exact ties
+    bias = rng.normal(0, 0.01, E).astype(np.float32)
+    ids = torch.zeros((T, k), dtype=torch.int32, device=cuda)
+    w = torch.zeros((T, k), dtype=torch.float32, device=cuda)
+    assert ops.k3_rocm_router_topk_f32_batch(ids, w, dev(logits, cuda), dev(bias, cuda), T, E, k,
+                                             scale)
+    sync()
+    want_ids, want_w = O.router_topk(logits, bias, k, scale)
+    np.testing.assert_array_equal(host(ids).view(np.uint32), want_ids)
+    np.testing.assert_array_equal(host(w), want_w)
+    # single-vector form
+    ids1 = torch.zeros(k, dtype=torch.int32, device=cuda)
+    w1 = torch.zeros(k, dtype=torch.float32, device=cuda)
+    assert ops.k3_rocm_router_topk_f32(ids1, w1, dev(logits[5], cuda), dev(bias, cuda), E, k, scale)
+    sync()
+    np.testing.assert_array_equal(host(ids1).view(np.uint32), want_ids[5])
+
+
+def test_activation_weighted_sum_add_copy(cuda):
+    rng = np.random.default_rng(3)
+    n = 4099
+    g = rand_bf16(rng, n, 3.0)
+    u = rand_bf16(rng, n, 30.0)
+    for kind in ("situ", "swiglu"):
+        out = torch.zeros(n, dtype=torch.int16, device=cuda)
+        if kind == "situ":
+            assert ops.k3_rocm_situ_bf16(out, dev(g.view(np.int16), cuda), dev(u.view(np.int16), cuda),
+                                         n, 4.0, 25.0)
+            want = O.situ(g, u)
+        else:
+            assert ops.k3_rocm_swiglu_bf16(out, dev(g.view(np.int16), cuda),
+                                           dev(u.view(np.int16), cuda), n)
+            want = O.swiglu(g, u)
+        sync()
+        np.testing.assert_array_equal(host(out).view(np.uint16), want)
+    T, K, H = 3, 16, 3584
+    v = rand_bf16(rng, (T, K, H))
+    w = rng.random((T, K)).astype(np.float32)
+    out = torch.zeros((T, H), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_weighted_sum_bf16_batch(out, dev(v.view(np.int16), cuda), dev(w, cuda), T, K, H)
+    sync()
+    np.testing.assert_array_equal(host(out).view(np.uint16), O.weighted_sum(v, w))
+    a = rand_bf16(rng, (T, H))
+    outa = torch.zeros((T, H), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_add_bf16(outa, dev(a.view(np.int16), cuda), out, T * H)
+    sync()
+    np.testing.assert_array_equal(host(outa).view(np.uint16),
+                                  O.add(a, host(out).view(np.uint16)))
+    rows = np.array([2, 0, 1], np.uint32)
+    gat = torch.zeros((3, H), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_gather_rows_bf16(gat, dev(a.view(np.int16), cuda), dev(rows.view(np.int32), cuda), 3, H)
+    sca = torch.zeros((3, H), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_scatter_rows_bf16(sca, gat, dev(rows.view(np.int32), cuda), 3, H)
+    sync()
+    np.testing.assert_array_equal(host(gat).view(np.uint16), a[rows])
+    np.testing.assert_array_equal(host(sca).view(np.uint16), a)
+
+
+@pytest.mark.skipif(not O.REF_OPS.exists(), reason="reference not built (oracle/_ref)")
+def test_against_reference_kernels(cuda):
+    """The reference's own kernels, built from its sources for gfx950, on the
+    same inputs: router ids equal given identical logits; MXFP4 within the
+    reference's bf16 tolerance (tests/test_k3_rocm_components.cu:323)."""
+    ref = ctypes.CDLL(str(O.REF_OPS))
+    rng = np.random.default_rng(11)
+    E, k, T = 896, 16, 8
+    logits = rng.normal(0, 1.7, (T, E)).astype(np.float32)
+    bias = rng.normal(0, 0.01, E).astype(np.float32)
+    ids_r = torch.zeros((T, k), dtype=torch.int32, device=cuda)
+    w_r = torch.zeros((T, k), dtype=torch.float32, device=cuda)
+    ids_m = torch.zeros_like(ids_r)
+    w_m = torch.zeros_like(w_r)
+    dl, db = dev(logits, cuda), dev(bias, cuda)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ref.k3_rocm_router_topk_f32_batch.restype = ctypes.c_bool
+    assert ref.k3_rocm_router_topk_f32_batch(
+        ctypes.c_void_p(ids_r.data_ptr()), ctypes.c_void_p(w_r.data_ptr()),
+        ctypes.c_void_p(dl.data_ptr()), ctypes.c_void_p(db.data_ptr()), T, E, k,
+        ctypes.c_float(2.5), st)
+    assert ops.k3_rocm_router_topk_f32_batch(ids_m, w_m, dl, db, T, E, k, 2.5)
+    sync()
+    assert torch.equal(ids_r, ids_m)
+    assert torch.allclose(w_r, w_m, rtol=0, atol=1e-6 * 2.5)
+    rows, cols = 128, 512
+    p, s = rand_mx(rng, rows, cols, 122, 132)
+    x = rand_bf16(rng, (1, cols))
+    o_r = torch.zeros(rows, dtype=torch.int16, device=cuda)
+    o_m = torch.zeros_like(o_r)
+    dp, ds, dx = dev(p, cuda), dev(s, cuda), dev(x.view(np.int16), cuda)
+    ref.k3_rocm_mxfp4_gemv_bf16.restype = ctypes.c_bool
+    assert ref.k3_rocm_mxfp4_gemv_bf16(ctypes.c_void_p(o_r.data_ptr()), ctypes.c_void_p(dp.data_ptr()),
+                                       ctypes.c_void_p(ds.data_ptr()), ctypes.c_void_p(dx.data_ptr()),
+                                       rows, cols, st)
+    assert ops.k3_rocm_mxfp4_gemv_bf16(o_m, dp, ds, dx, rows, cols)
+    sync()
+    a = bf16_bits_to_f32(host(o_r).view(np.uint16))
+    b = bf16_bits_to_f32(host(o_m).view(np.uint16))
+    _, f64 = O.mxfp4_gemm(p, s, x, rows, cols, O.ORDER_F64)
+    scale = np.maximum(np.abs(f64[0]), 1.0)
+    assert np.max(np.abs(a - b) / scale) <= 2 * 2.0 ** -8
