@@ -75,6 +75,14 @@ typedef struct {
 size_t k3_moe_workspace_bytes(const k3_moe_shape *shape, uint32_t token_count);
 
 /*
+ * Prepares a freshly allocated workspace (zeroes the arrival counter of the
+ * decode router kernel; every later call leaves it zero again). Call once
+ * per workspace before its first use, on the stream that uses it.
+ */
+bool k3_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+
+/*
  * Device routing plan (replaces the host loop at
  * k3_engine_prefill.inc:1175-1194). For every selected expert in
  * ascending id, rows in (token asc, rank asc) order: a stable sort of the

@@ -73,6 +73,7 @@ SIGNATURES = {
     "k3_rocm_scatter_rows_bf16": (_b, [_p, _p, _p, _u32, _u32, _p]),
     "k3_rocm_add_bf16": (_b, [_p, _p, _p, _u64, _p]),
     "k3_moe_workspace_bytes": (_sz, [ctypes.POINTER(K3MoeShape), _u32]),
+    "k3_moe_workspace_init": (_b, [_p, _sz, _p]),
     "k3_moe_plan_scratch_bytes": (_sz, [_u32, _u32]),
     "k3_moe_route_plan": (_b, [_p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _p, _sz, _p]),
     "k3_moe_forward_bf16": (_b, [_p, _p, _p, _p, _p, _p, ctypes.POINTER(K3MoeShape), _u32,

@@ -25,6 +25,18 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) {
     return __uint_as_float(w & 0xffff0000u);
 }
 
+/* Global-address-space view of a pointer that came from memory (expert
+ * tables): lets the compiler emit global_load with a scalar base instead of
+ * flat_load with 64-bit per-lane addresses. */
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gload(const uint4 *p) {
+    const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t gload(const uint8_t *p) {
+    return *(const __attribute__((address_space(1))) uint8_t *)p;
+}
+
 /* Round to nearest even; NaN stays a quiet NaN (hip_bfloat16 semantics). */
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);
@@ -157,32 +169,37 @@ __device__ __forceinline__ float wave_sum(float v) {
  * Reduce N per-lane partials (N a power of two, <= 64) over the wave in one
  * transpose-reduce: at stage o each lane keeps half of its rows and adds
  * the partner's copy. Every row ends up with exactly the butterfly64 value
- * (same pairings, fp32 add is commutative). Row i's sum is returned in
- * lanes whose position selects row i: lane bits (5..) pick the row as
- * computed by wave_rows_owner().
+ * (same pairings, fp32 add is commutative). Which row a lane holds at the
+ * end is given by wave_rows_owner<N>(). All indices are compile-time.
  */
+template <int N, int O>
+struct RowReduce {
+    static __device__ __forceinline__ float run(float *p, int lane) {
+        if constexpr (O == 0) {
+            return p[0];
+        } else if constexpr (N > 1) {
+            constexpr int H = N / 2;
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < H; i++) {
+                const float send = upper ? p[i] : p[i + H];
+                const float keep = upper ? p[i + H] : p[i];
+                p[i] = __fadd_rn(keep, __shfl_xor(send, O, 64));
+            }
+            return RowReduce<H, O / 2>::run(p, lane);
+        } else {
+            float v = p[0];
+#pragma unroll
+            for (int o = O; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
+            return v;
+        }
+    }
+};
+
 template <int N>
 __device__ __forceinline__ float wave_sum_rows(float (&p)[N]) {
-    const int lane = threadIdx.x & 63;
-    int n = N;
-    int o = 32;
-    /* stages that halve the row set */
-#pragma unroll
-    for (; n > 1 && o >= 1; o >>= 1) {
-        const bool upper = (lane & o) != 0;
-        const int half = n / 2;
-#pragma unroll
-        for (int i = 0; i < half; i++) {
-            const float send = upper ? p[i] : p[i + half];
-            const float keep = upper ? p[i + half] : p[i];
-            const float recv = __shfl_xor(send, o, 64);
-            p[i] = __fadd_rn(keep, recv);
-        }
-        n = half;
-    }
-    float v = p[0];
-    for (; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, 64));
-    return v;
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+    return RowReduce<N, 32>::run(p, (int)(threadIdx.x & 63u));
 }
 
 /* Which row of wave_sum_rows<N> a lane holds at the end. */

@@ -7,11 +7,8 @@
  *
  *   router logits (bf16 -> f32, w64 order)        k3_rocm_bf16_gemm_f32
  *   top-k (sigmoid + bias, lowest-id ties)        k3_rocm_router_topk_f32_batch
- *   T == 1: decode_gateup_kernel   16 experts x F rows, gate and up of a
- *                                  row in one wave, activation fused
- *           decode_down_kernel     one block per 8 output rows reads the
- *                                  row for all k experts and fuses the
- *                                  weighted combine and the residual add
+ *   T == 1: the three decode kernels of k3_decode.hip (router + top-k,
+ *           gate/up + activation, down + combine + residual)
  *   T  > 1: device routing plan (count -> scan -> stable scatter), then
  *           grouped gate/up and down over the selected experts only (each
  *           expert's weights are read once per row block for all its
@@ -23,6 +20,7 @@
  */
 #include "k3_device.h"
 #include "k3_internal.h"
+#include "k3_decode.h"
 #include "../../include/k3_moe.h"
 #include "../../include/k3_rocm_ops.h"
 
@@ -43,13 +41,17 @@ inline size_t align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
 /* ------------------------------------------------------------------------ */
 
 struct Workspace {
+    DecodeSync *sync;
     float *logits;
+    float *scores;
+    uint32_t *keys;
     uint32_t *ids;
     float *weights;
     uint32_t *counts, *offsets, *unique, *summary;
     uint32_t *token_index, *route_index;
     uint32_t *chunk_base;
     uint16_t *act;
+    uint16_t *slot_out;
     uint16_t *y;
     size_t bytes;
 };
@@ -68,7 +70,10 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
         return r;
     };
     const uint64_t routes = (uint64_t)T * s.top_k;
+    w.sync = (DecodeSync *)take(sizeof(DecodeSync));
     w.logits = (float *)take(4ull * T * s.expert_count);
+    w.scores = (float *)take(4ull * s.expert_count);
+    w.keys = (uint32_t *)take(4ull * s.expert_count);
     w.ids = (uint32_t *)take(4ull * routes);
     w.weights = (float *)take(4ull * routes);
     w.counts = (uint32_t *)take(4ull * s.expert_count);
@@ -79,6 +84,7 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
     w.route_index = (uint32_t *)take(4ull * routes);
     w.chunk_base = (uint32_t *)take(plan_scratch(T, s.expert_count));
     w.act = (uint16_t *)take(2ull * routes * s.ffn);
+    w.slot_out = (uint16_t *)take(T == 1u ? 2ull * s.top_k * s.hidden : 0u);
     w.y = (uint16_t *)take(T > 1u ? 2ull * routes * s.hidden : 0u);
     w.bytes = off;
     return w;
@@ -205,121 +211,7 @@ bool launch_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique, uint32_t
     return hipGetLastError() == hipSuccess;
 }
 
-/* ------------------------------------------------------------------------ */
-/* decode (one token)                                                        */
-/* ------------------------------------------------------------------------ */
-
 __device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
-
-/*
- * grid (F / (4 * RW), k), block 256. Wave w of block b computes rows
- * [RW*(4b+w), +RW) of both gate and up for expert ids[slot], then applies
- * the activation to the bf16-rounded pair (k3_engine.cu:1032-1057).
- * Lane l walks groups l, l+64, ... ; per group the 32 activations are
- * converted once and reused for all 2*RW rows.
- */
-template <int RW>
-__global__ __launch_bounds__(256) void decode_gateup_kernel(
-        uint16_t *__restrict__ act, const uint16_t *__restrict__ x,
-        const uint32_t *__restrict__ ids, const k3_moe_expert *__restrict__ experts,
-        uint32_t H, uint32_t F, uint32_t E, uint32_t kind, float beta, float lb) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t slot = blockIdx.y;
-    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
-    const uint32_t e = ids[slot];
-    if (row0 >= F) return;
-    uint16_t *dst = act + (uint64_t)slot * F + row0;
-    if (e >= E) {
-        if (lane < (uint32_t)RW) dst[lane] = 0;
-        return;
-    }
-    const k3_moe_expert ex = experts[e];
-    const uint32_t G = H / 32u;
-    const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u);
-    const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u);
-    const uint8_t *gsc = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G;
-    const uint8_t *usc = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G;
-    const uint4 *x4 = (const uint4 *)x;
-    float acc[2 * RW];
-#pragma unroll
-    for (int i = 0; i < 2 * RW; i++) acc[i] = 0.0f;
-    for (uint32_t g = lane; g < G; g += 64u) {
-        uint4 w[2 * RW];
-        uint32_t sc[2 * RW];
-#pragma unroll
-        for (int i = 0; i < RW; i++) {
-            w[i] = *(const uint4 *)(gp + (uint64_t)i * (H / 2u) + 16u * g);
-            w[RW + i] = *(const uint4 *)(up + (uint64_t)i * (H / 2u) + 16u * g);
-            sc[i] = gsc[(uint64_t)i * G + g];
-            sc[RW + i] = usc[(uint64_t)i * G + g];
-        }
-        float xf[32];
-        bf16x32_to_f32(x4 + 4u * g, xf);
-#pragma unroll
-        for (int i = 0; i < 2 * RW; i++)
-            acc[i] = fmaf(fp4_group(w[i], xf), e8m0_to_f32(sc[i]), acc[i]);
-    }
-    const float v = wave_sum_rows<2 * RW>(acc);
-    const float u = __shfl_xor(v, 32, 64);
-    const int owner = wave_rows_owner<2 * RW>();
-    if (lane < 32u && (lane & (64u / (2u * RW) - 1u)) == 0u)
-        dst[owner] = f32_to_bf16(gated_act(bf16_round(v), bf16_round(u), kind, beta, lb));
-}
-
-/*
- * grid (H / RB), block 64 * k. Wave s computes RB consecutive output rows
- * of the down projection for slot s; the block then combines the k bf16
- * slot outputs in rank order and adds the residual (k3_rocm_ops.cu:
- * 1452-1510 semantics).
- */
-template <int RB>
-__global__ __launch_bounds__(1024) void decode_down_kernel(
-        uint16_t *__restrict__ out, const uint16_t *__restrict__ act,
-        const uint16_t *__restrict__ residual, const uint32_t *__restrict__ ids,
-        const float *__restrict__ wts, const k3_moe_expert *__restrict__ experts, uint32_t H,
-        uint32_t F, uint32_t E, uint32_t k) {
-    __shared__ float ybuf[32][RB];
-    const uint32_t lane = threadIdx.x & 63u, slot = threadIdx.x >> 6;
-    const uint32_t row0 = blockIdx.x * RB;
-    const uint32_t e = ids[slot];
-    const uint32_t G = F / 32u;
-    float acc[RB];
-#pragma unroll
-    for (int i = 0; i < RB; i++) acc[i] = 0.0f;
-    if (e < E) {
-        const k3_moe_expert ex = experts[e];
-        const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
-        const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
-        const uint4 *a4 = (const uint4 *)(act + (uint64_t)slot * F);
-        for (uint32_t g = lane; g < G; g += 64u) {
-            uint4 w[RB];
-            uint32_t sc[RB];
-#pragma unroll
-            for (int i = 0; i < RB; i++) {
-                w[i] = *(const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g);
-                sc[i] = ds[(uint64_t)i * G + g];
-            }
-            float xf[32];
-            bf16x32_to_f32(a4 + 4u * g, xf);
-#pragma unroll
-            for (int i = 0; i < RB; i++)
-                acc[i] = fmaf(fp4_group(w[i], xf), e8m0_to_f32(sc[i]), acc[i]);
-        }
-    }
-    const float v = wave_sum_rows<RB>(acc);
-    const int owner = wave_rows_owner<RB>();
-    if ((lane & (64u / RB - 1u)) == 0u) ybuf[slot][owner] = bf16_round(v);
-    __syncthreads();
-    if (threadIdx.x < (uint32_t)RB) {
-        const uint32_t row = row0 + threadIdx.x;
-        float c = 0.0f;
-        for (uint32_t s = 0; s < k; s++)
-            if (ids[s] < E) c = __fadd_rn(c, __fmul_rn(wts[s], ybuf[s][threadIdx.x]));
-        const float cb = bf16_round(c);
-        out[row] = residual ? f32_to_bf16(__fadd_rn(bf16_to_f32(residual[row]), cb))
-                            : f32_to_bf16(cb);
-    }
-}
 
 /* ------------------------------------------------------------------------ */
 /* grouped (many tokens), exact order                                        */
@@ -497,37 +389,50 @@ bool shape_ok(const k3_moe_shape *s) {
            (s->activation == 1u || (s->beta > 0.0f && s->linear_beta > 0.0f));
 }
 
-struct Marker {
-    const k3_moe_profile *profile;
-    hipStream_t stream;
-    void operator()(int stage) const {
-        if (profile && profile->stage_events[stage])
-            (void)hipEventRecord((hipEvent_t)profile->stage_events[stage], stream);
-    }
-};
+DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden,
+                           const void *residual, const void *router_weight,
+                           const void *router_bias, const k3_moe_expert *experts,
+                           const k3_moe_shape &s, void *ids_copy, void *w_copy) {
+    DecodeParams P{};
+    P.output = (uint16_t *)output;
+    P.residual = (const uint16_t *)residual;
+    P.hidden_in = (const uint16_t *)hidden;
+    P.router_weight = (const uint16_t *)router_weight;
+    P.router_bias = (const float *)router_bias;
+    P.experts = experts;
+    P.logits = ws.logits;
+    P.scores = ws.scores;
+    P.keys = ws.keys;
+    P.ids = ws.ids;
+    P.weights = ws.weights;
+    P.ids_copy = (uint32_t *)ids_copy;
+    P.weights_copy = (float *)w_copy;
+    P.act = ws.act;
+    P.slot_out = ws.slot_out;
+    P.down_arrive = ws.sync->down_arrive;
+    P.sync = ws.sync;
+    P.hidden = s.hidden;
+    P.ffn = s.ffn;
+    P.expert_count = s.expert_count;
+    P.top_k = s.top_k;
+    P.scale = s.scaling_factor;
+    P.activation = s.activation;
+    P.beta = s.activation == 1u ? 1.0f : s.beta;
+    P.linear_beta = s.activation == 1u ? 1.0f : s.linear_beta;
+    return P;
+}
 
 /* Expert stage on routes already in ws.ids / ws.weights. */
 bool run_experts(const Workspace &ws, void *output, const void *hidden, const void *residual,
                  const k3_moe_expert *experts, const k3_moe_shape &s, uint32_t T,
-                 hipStream_t st, const Marker &mark) {
+                 hipStream_t st, const StageMarker &mark) {
     const uint32_t H = s.hidden, F = s.ffn, E = s.expert_count, k = s.top_k;
     const float beta = s.activation == 1u ? 1.0f : s.beta;
     const float lb = s.activation == 1u ? 1.0f : s.linear_beta;
-    if (T == 1u && k <= 16u) {
-        mark(K3_MOE_STAGE_PLAN);
-        mark(K3_MOE_STAGE_GATE_UP);
-        constexpr int RW = 4;
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_gateup_kernel<RW>), dim3(F / (4u * RW), k),
-                           dim3(256), 0, st, ws.act, (const uint16_t *)hidden, ws.ids, experts,
-                           H, F, E, s.activation, beta, lb);
-        constexpr int RB = 8;
-        mark(K3_MOE_STAGE_DOWN);
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(decode_down_kernel<RB>), dim3(H / RB), dim3(64u * k),
-                           0, st, (uint16_t *)output, ws.act, (const uint16_t *)residual, ws.ids,
-                           ws.weights, experts, H, F, E, k);
-        mark(K3_MOE_STAGE_COMBINE);
-        mark(K3_MOE_STAGE_END);
-        return hipGetLastError() == hipSuccess;
+    if (T == 1u && decode_supported(s)) {
+        const DecodeParams P = decode_params(ws, output, hidden, residual, nullptr, nullptr,
+                                             experts, s, nullptr, nullptr);
+        return decode_launch_experts(P, st, mark);
     }
     mark(K3_MOE_STAGE_PLAN);
     if (!launch_plan(ws.counts, ws.offsets, ws.unique, ws.summary, ws.token_index,
@@ -561,6 +466,12 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
 extern "C" size_t k3_moe_workspace_bytes(const k3_moe_shape *shape, uint32_t token_count) {
     if (!shape_ok(shape) || token_count == 0u || token_count > 65535u) return 0u;
     return carve(nullptr, *shape, token_count).bytes;
+}
+
+extern "C" bool k3_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
+    if (!workspace || workspace_bytes < sizeof(DecodeSync)) return false;
+    /* the counters sit at the start of every workspace layout */
+    return decode_init_sync((DecodeSync *)workspace, (hipStream_t)stream);
 }
 
 extern "C" size_t k3_moe_plan_scratch_bytes(uint32_t token_count, uint32_t expert_count) {
@@ -599,7 +510,7 @@ extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void
             hipSuccess)
         return false;
     return run_experts(ws, output, hidden, residual, experts, *shape, token_count, st,
-                       Marker{nullptr, st});
+                       StageMarker{nullptr, st});
 }
 
 extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, const void *residual,
@@ -616,7 +527,13 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
     Workspace ws = carve(workspace, *shape, token_count);
     if (workspace_bytes < ws.bytes) return false;
     const hipStream_t st = (hipStream_t)stream;
-    const Marker mark{profile, st};
+    const StageMarker mark{profile, st};
+    if (token_count == 1u && decode_supported(*shape) && ((uintptr_t)router_weight % 16u) == 0u) {
+        const DecodeParams P = decode_params(ws, output, hidden, residual, router_weight,
+                                             router_bias, experts, *shape, expert_ids,
+                                             expert_weights);
+        return decode_launch(P, st, mark);
+    }
     mark(K3_MOE_STAGE_ROUTER);
     if (!launch_bf16_rows_f32_any(ws.logits, router_weight, hidden, token_count,
                                   shape->expert_count, shape->hidden, st) ||

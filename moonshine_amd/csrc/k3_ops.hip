@@ -15,6 +15,7 @@
  */
 #include "k3_device.h"
 #include "k3_internal.h"
+#include "k3_topk.h"
 #include "../../include/k3_rocm_ops.h"
 
 #include <hip/hip_runtime.h>
@@ -103,76 +104,33 @@ bool launch_bf16_rows_f32(void *out, const void *w, const void *x, uint32_t toke
 /* router top-k                                                              */
 /* ------------------------------------------------------------------------ */
 
-/* (choice desc, id asc) total order; NaN choices never win. */
-__device__ __forceinline__ bool better(float c, uint32_t id, float bc, uint32_t bid) {
-    if (c != c) return false;
-    if (bid == UINT32_MAX) return true;
-    return c > bc || (c == bc && id < bid);
-}
-
-/*
- * One block per token. Scores and choices are computed once per expert,
- * then top_k rounds of a block-wide arg-max under (choice desc, id asc)
- * produce the ids in rank order; this is the same order as the reference's
- * bitonic sort read from the end (k3_rocm_ops.cu:1397-1437).
- */
+/* One wave per token (4 tokens per block): sigmoid, choice keys and the
+ * wave radix select of k3_topk.h. */
 __global__ __launch_bounds__(256) void router_topk_kernel(
         uint32_t *__restrict__ ids_out, float *__restrict__ w_out,
         uint32_t *ids_copy, float *w_copy,
         const float *__restrict__ logits, const float *__restrict__ bias,
-        uint32_t experts, uint32_t top_k, float scale) {
-    __shared__ float s_score[1024];
-    __shared__ float s_choice[1024];
-    __shared__ float r_choice[4];
-    __shared__ uint32_t r_id[4];
-    __shared__ uint32_t sel_id[64];
-    __shared__ float sel_score[64];
-    const uint32_t t = blockIdx.x;
-    const float *lg = logits + (uint64_t)t * experts;
-    for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) {
-        const float s = det_sigmoid(lg[e]);
-        s_score[e] = s;
-        s_choice[e] = __fadd_rn(s, bias[e]);
-    }
-    __syncthreads();
+        uint32_t tokens, uint32_t experts, uint32_t top_k, float scale) {
+    __shared__ TopkWaveSmem sm[4];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    for (uint32_t r = 0; r < top_k; r++) {
-        float bc = 0.0f;
-        uint32_t bid = UINT32_MAX;
-        for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x)
-            if (better(s_choice[e], e, bc, bid)) { bc = s_choice[e]; bid = e; }
+    const uint32_t t = blockIdx.x * 4u + wave;
+    if (t >= tokens) return;
+    const float *lg = logits + (uint64_t)t * experts;
+    uint32_t key[kTopkSlots];
+    float score[kTopkSlots];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float oc = __shfl_xor(bc, o, 64);
-            const uint32_t oid = __shfl_xor(bid, o, 64);
-            if (oid != UINT32_MAX && better(oc, oid, bc, bid)) { bc = oc; bid = oid; }
-        }
-        if (lane == 0u) { r_choice[wave] = bc; r_id[wave] = bid; }
-        __syncthreads();
-        if (threadIdx.x == 0u) {
-            float c = r_choice[0];
-            uint32_t id = r_id[0];
-            for (uint32_t w = 1; w < blockDim.x / 64u; w++)
-                if (r_id[w] != UINT32_MAX && better(r_choice[w], r_id[w], c, id)) {
-                    c = r_choice[w]; id = r_id[w];
-                }
-            sel_id[r] = id;
-            sel_score[r] = id == UINT32_MAX ? 0.0f : s_score[id];
-            if (id != UINT32_MAX) s_choice[id] = __builtin_nanf("");
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0u) {
-        float den = 1e-20f;
-        for (uint32_t r = 0; r < top_k; r++) den = __fadd_rn(den, sel_score[r]);
-        for (uint32_t r = 0; r < top_k; r++) {
-            const float wr = __fmul_rn(__fdiv_rn(sel_score[r], den), scale);
-            ids_out[(uint64_t)t * top_k + r] = sel_id[r];
-            w_out[(uint64_t)t * top_k + r] = wr;
-            if (ids_copy) ids_copy[(uint64_t)t * top_k + r] = sel_id[r];
-            if (w_copy) w_copy[(uint64_t)t * top_k + r] = wr;
+    for (int j = 0; j < kTopkSlots; j++) {
+        const uint32_t e = lane + 64u * j;
+        key[j] = 0u;
+        score[j] = 0.0f;
+        if (e < experts) {
+            score[j] = det_sigmoid(lg[e]);
+            key[j] = choice_key(score[j], bias[e]);
         }
     }
+    const uint64_t o = (uint64_t)t * top_k;
+    topk_select_wave(key, score, top_k, scale, ids_out + o, w_out + o,
+                     ids_copy ? ids_copy + o : nullptr, w_copy ? w_copy + o : nullptr, sm[wave]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -310,8 +268,8 @@ bool k3::launch_bf16_rows_f32_any(float *out, const void *w, const void *x, uint
 bool k3::launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,
                             const float *logits, const float *bias, uint32_t tokens,
                             uint32_t experts, uint32_t top_k, float scale, hipStream_t s) {
-    hipLaunchKernelGGL(router_topk_kernel, dim3(tokens), dim3(256), 0, s, ids, w, ids2, w2,
-                       logits, bias, experts, top_k, scale);
+    hipLaunchKernelGGL(router_topk_kernel, dim3((tokens + 3u) / 4u), dim3(256), 0, s, ids, w, ids2,
+                       w2, logits, bias, tokens, experts, top_k, scale);
     return hipGetLastError() == hipSuccess;
 }
 

@@ -98,6 +98,9 @@ class RoutedMoE:
             raise ValueError("unsupported shape or token count")
         if self._ws is None or self._ws.numel() < need:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.router_weight.device)
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            if not lib().k3_moe_workspace_init(ctypes.c_void_p(self._ws.data_ptr()), need, st):
+                raise RuntimeError("k3_moe_workspace_init failed")
         return self._ws
 
     def forward(self, hidden, residual=None, out=None, ids=None, weights=None,

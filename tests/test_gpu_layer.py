@@ -40,6 +40,24 @@ def run(cfg, inputs, moe, cuda):
     return (L.bf16_bits(out), ids.cpu().numpy().view(np.uint32), w.cpu().numpy())
 
 
+def run_profiled(cfg, inputs, moe, cuda):
+    """k3_moe_forward_profiled_bf16 with (unset) stage events."""
+    from moonshine_amd._lib import K3MoeProfile
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    T = x.shape[0]
+    out = torch.empty_like(x)
+    ws = moe.workspace(T)
+    prof = K3MoeProfile()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert lib().k3_moe_forward_profiled_bf16(
+        P(out), P(x), P(r), P(moe.router_weight), P(moe.router_bias), P(moe.store.table),
+        ctypes.byref(moe.shape), T, 0, None, None, P(ws), ws.numel(), ctypes.byref(prof),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return L.bf16_bits(out)
+
+
 def host_experts(store, ids):
     return {int(e): store.host_expert(int(e)) for e in np.unique(ids)}
 
@@ -80,6 +98,12 @@ def test_decode_layer_bitexact(cuda, cfg):
     np.testing.assert_array_equal(out, want["output"])
     assert len(set(ids[0].tolist())) == cfg.top_k
     np.testing.assert_allclose(w.sum(), cfg.scale, rtol=1e-6)
+    # the profiled entry point gives the same bits
+    np.testing.assert_array_equal(run_profiled(cfg, inputs, moe, cuda), want["output"])
+    # repeated calls reuse the workspace (arrival counter reset by the kernel)
+    for _ in range(3):
+        o2, i2, _ = run(cfg, inputs, moe, cuda)
+        np.testing.assert_array_equal(o2, out)
 
 
 @pytest.mark.parametrize("cfg_index,check", [(0, None), (2, 12), (3, 6)])
