@@ -75,12 +75,11 @@ typedef struct {
 size_t k3_moe_workspace_bytes(const k3_moe_shape *shape, uint32_t token_count);
 
 /*
- * Prepares a freshly allocated workspace (zeroes the arrival counter of the
- * decode router kernel; every later call leaves it zero again). Call once
- * per workspace before its first use, on the stream that uses it.
+ * Prepares a freshly allocated workspace. The current kernels keep no state
+ * in the workspace between calls, so this only validates the arguments; it
+ * is part of the contract so later versions may keep counters there.
  */
 bool k3_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
-
 
 /*
  * Device routing plan (replaces the host loop at

@@ -8,16 +8,6 @@
 
 namespace k3 {
 
-/* Arrival counters of the decode kernels: zero between calls
- * (k3_moe_workspace_init zeroes them once; the last block to arrive at each
- * counter resets it). */
-constexpr uint32_t kMaxDownRowBlocks = 16384; /* hidden / 8 */
-struct DecodeSync {
-    uint32_t arrive_router;
-    uint32_t pad[63];
-    uint32_t down_arrive[kMaxDownRowBlocks];
-};
-
 struct DecodeParams {
     uint16_t *output;
     const uint16_t *residual;
@@ -32,10 +22,8 @@ struct DecodeParams {
     float *weights;
     uint32_t *ids_copy;
     float *weights_copy;
-    uint16_t *act;
-    uint16_t *slot_out;     /* [k, hidden] bf16 down outputs */
-    uint32_t *down_arrive;  /* = sync->down_arrive */
-    DecodeSync *sync;
+    uint16_t *act;          /* [k, ffn] bf16 activations */
+    k3_moe_expert *sel;     /* [k] descriptors of the selected experts */
     uint32_t hidden, ffn, expert_count, top_k;
     float scale;
     uint32_t activation;
@@ -52,10 +40,12 @@ struct StageMarker {
 };
 
 bool decode_supported(const k3_moe_shape &s);
-bool decode_init_sync(DecodeSync *sync, hipStream_t stream);
-/* router + top-k, gate/up, down + combine */
+/* router, top-k, gate/up, down, combine */
 bool decode_launch(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
-/* gate/up, down + combine on routes already in p.ids / p.weights */
-bool decode_launch_experts(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
+/* gate/up, down, combine on routes in p.ids / p.weights (resolve: look the
+ * expert descriptors up first, for routes that did not come from
+ * decode_launch's top-k) */
+bool decode_launch_experts(const DecodeParams &p, hipStream_t stream, const StageMarker &mark,
+                           bool resolve);
 
 }  // namespace k3

@@ -41,7 +41,6 @@ inline size_t align256(size_t v) { return (v + 255u) & ~(size_t)255u; }
 /* ------------------------------------------------------------------------ */
 
 struct Workspace {
-    DecodeSync *sync;
     float *logits;
     float *scores;
     uint32_t *keys;
@@ -51,7 +50,7 @@ struct Workspace {
     uint32_t *token_index, *route_index;
     uint32_t *chunk_base;
     uint16_t *act;
-    uint16_t *slot_out;
+    k3_moe_expert *sel;
     uint16_t *y;
     size_t bytes;
 };
@@ -70,7 +69,6 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
         return r;
     };
     const uint64_t routes = (uint64_t)T * s.top_k;
-    w.sync = (DecodeSync *)take(sizeof(DecodeSync));
     w.logits = (float *)take(4ull * T * s.expert_count);
     w.scores = (float *)take(4ull * s.expert_count);
     w.keys = (uint32_t *)take(4ull * s.expert_count);
@@ -84,7 +82,7 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
     w.route_index = (uint32_t *)take(4ull * routes);
     w.chunk_base = (uint32_t *)take(plan_scratch(T, s.expert_count));
     w.act = (uint16_t *)take(2ull * routes * s.ffn);
-    w.slot_out = (uint16_t *)take(T == 1u ? 2ull * s.top_k * s.hidden : 0u);
+    w.sel = (k3_moe_expert *)take(T == 1u ? sizeof(k3_moe_expert) * s.top_k : 0u);
     w.y = (uint16_t *)take(T > 1u ? 2ull * routes * s.hidden : 0u);
     w.bytes = off;
     return w;
@@ -408,9 +406,7 @@ DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden
     P.ids_copy = (uint32_t *)ids_copy;
     P.weights_copy = (float *)w_copy;
     P.act = ws.act;
-    P.slot_out = ws.slot_out;
-    P.down_arrive = ws.sync->down_arrive;
-    P.sync = ws.sync;
+    P.sel = ws.sel;
     P.hidden = s.hidden;
     P.ffn = s.ffn;
     P.expert_count = s.expert_count;
@@ -432,7 +428,7 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
     if (T == 1u && decode_supported(s)) {
         const DecodeParams P = decode_params(ws, output, hidden, residual, nullptr, nullptr,
                                              experts, s, nullptr, nullptr);
-        return decode_launch_experts(P, st, mark);
+        return decode_launch_experts(P, st, mark, true);
     }
     mark(K3_MOE_STAGE_PLAN);
     if (!launch_plan(ws.counts, ws.offsets, ws.unique, ws.summary, ws.token_index,
@@ -469,9 +465,9 @@ extern "C" size_t k3_moe_workspace_bytes(const k3_moe_shape *shape, uint32_t tok
 }
 
 extern "C" bool k3_moe_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
-    if (!workspace || workspace_bytes < sizeof(DecodeSync)) return false;
-    /* the counters sit at the start of every workspace layout */
-    return decode_init_sync((DecodeSync *)workspace, (hipStream_t)stream);
+    if (!workspace || workspace_bytes == 0u) return false;
+    (void)stream;
+    return true;
 }
 
 extern "C" size_t k3_moe_plan_scratch_bytes(uint32_t token_count, uint32_t expert_count) {

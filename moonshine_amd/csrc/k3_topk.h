@@ -51,13 +51,15 @@ __device__ __forceinline__ void wave_fence() {
 }
 
 /* key[j]/score[j] for expert lane + 64 j. Writes ids/weights[0..top_k) (and
- * the optional copies). Must be called by all 64 lanes of the wave;
- * top_k <= 32. */
+ * the optional copies, which may be host-mapped). Must be called by all 64
+ * lanes of the wave; top_k <= 32. With `publish`, ids/weights are written
+ * with write-through agent-scope stores (for readers in the same kernel). */
 __device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlots],
                                                  const float (&score)[kTopkSlots],
                                                  uint32_t top_k, float scale, uint32_t *ids,
                                                  float *weights, uint32_t *ids_copy,
-                                                 float *w_copy, TopkWaveSmem &sm) {
+                                                 float *w_copy, TopkWaveSmem &sm,
+                                                 bool publish = false) {
     const uint32_t lane = threadIdx.x & 63u;
     const unsigned long long below = (1ull << lane) - 1ull;
     /* Threshold: the top_k-th largest lane maximum M. The top_k lanes with
@@ -69,6 +71,7 @@ __device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlot
     sm.lmax[lane] = lmax;
     wave_fence();
     uint32_t r = 0u;
+#pragma unroll
     for (uint32_t i = 0; i < 64u; i++) {
         const uint32_t v = sm.lmax[i];
         r += (v > lmax || (v == lmax && i < lane)) ? 1u : 0u;
@@ -98,10 +101,14 @@ __device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlot
         const bool live = c < ncand;
         const uint32_t mk = live ? sm.cand_key[c] : 0u, mi = live ? sm.cand_id[c] : 0u;
         uint32_t cnt = live ? 0u : top_k;
-        for (uint32_t i = 0; i < ncand; i++) {
-            const uint32_t ok = sm.cand_key[i], oi = sm.cand_id[i];
-            cnt += (ok > mk || (ok == mk && oi < mi)) ? 1u : 0u;
-            if ((i & 15u) == 15u && __ballot(cnt < top_k) == 0ull) break;
+        for (uint32_t i0 = 0; i0 < ncand; i0 += 16u) {
+#pragma unroll
+            for (uint32_t i = i0; i < i0 + 16u; i++) {
+                const uint32_t ok = i < ncand ? sm.cand_key[i] : 0u;
+                const uint32_t oi = sm.cand_id[i < ncand ? i : 0u];
+                cnt += (i < ncand && (ok > mk || (ok == mk && oi < mi))) ? 1u : 0u;
+            }
+            if (__ballot(cnt < top_k) == 0ull) break;
         }
         if (cnt < top_k) {
             sm.out_id[cnt] = mi;
@@ -110,17 +117,23 @@ __device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlot
     }
     wave_fence();
     const uint32_t nsel = ncand < top_k ? ncand : top_k;
-    float den = 0.0f;
-    if (lane == 0u) {
-        den = 1e-20f;
-        for (uint32_t q = 0; q < top_k; q++) den = __fadd_rn(den, q < nsel ? sm.out_score[q] : 0.0f);
-    }
-    den = __shfl(den, 0, 64);
+    /* lane r holds the rank-r score; the denominator adds them in rank
+     * order (a sequential chain over lane reads) */
+    const float my_score = lane < nsel ? sm.out_score[lane] : 0.0f;
+    float den = 1e-20f;
+    for (uint32_t q = 0; q < top_k; q++)
+        den = __fadd_rn(den, __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                 __builtin_bit_cast(int, my_score), (int)q)));
     if (lane < top_k) {
         const uint32_t id = lane < nsel ? sm.out_id[lane] : UINT32_MAX;
-        const float wr = __fmul_rn(__fdiv_rn(lane < nsel ? sm.out_score[lane] : 0.0f, den), scale);
-        ids[lane] = id;
-        weights[lane] = wr;
+        const float wr = __fmul_rn(__fdiv_rn(my_score, den), scale);
+        if (publish) {
+            __hip_atomic_store(ids + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(weights + lane, wr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            ids[lane] = id;
+            weights[lane] = wr;
+        }
         if (ids_copy) ids_copy[lane] = id;
         if (w_copy) w_copy[lane] = wr;
     }

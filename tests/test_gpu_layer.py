@@ -41,7 +41,7 @@ def run(cfg, inputs, moe, cuda):
 
 
 def run_profiled(cfg, inputs, moe, cuda):
-    """k3_moe_forward_profiled_bf16 with (unset) stage events."""
+    """k3_moe_forward_profiled_bf16 with every stage event set."""
     from moonshine_amd._lib import K3MoeProfile
     x = L.bf16_tensor(inputs.hidden, cuda)
     r = L.bf16_tensor(inputs.residual, cuda)
@@ -49,6 +49,13 @@ def run_profiled(cfg, inputs, moe, cuda):
     out = torch.empty_like(x)
     ws = moe.workspace(T)
     prof = K3MoeProfile()
+    hip = ctypes.CDLL("libamdhip64.so")
+    events = []
+    for i in range(7):
+        e = ctypes.c_void_p()
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+        prof.stage_events[i] = e.value
+        events.append(e)
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     assert lib().k3_moe_forward_profiled_bf16(
         P(out), P(x), P(r), P(moe.router_weight), P(moe.router_bias), P(moe.store.table),
@@ -98,12 +105,21 @@ def test_decode_layer_bitexact(cuda, cfg):
     np.testing.assert_array_equal(out, want["output"])
     assert len(set(ids[0].tolist())) == cfg.top_k
     np.testing.assert_allclose(w.sum(), cfg.scale, rtol=1e-6)
-    # the profiled entry point gives the same bits
+    # the profiled entry point (stage events recorded) gives the same bits
     np.testing.assert_array_equal(run_profiled(cfg, inputs, moe, cuda), want["output"])
-    # repeated calls reuse the workspace (arrival counter reset by the kernel)
+    # repeated calls reuse the workspace; alternate with a second token so
+    # stale routes or activations would show
+    other = make_inputs(cfg, seed=cfg.seed + 77)
+    want2 = O.layer(cfg, other, host_experts(moe.store, O.router_topk(
+        O.router_logits(other.router_weight, other.hidden), other.router_bias, cfg.top_k,
+        cfg.scale)[0]))
+    moe2 = L.build_layer(cfg, other, device=cuda, store=moe.store)
     for _ in range(3):
         o2, i2, _ = run(cfg, inputs, moe, cuda)
         np.testing.assert_array_equal(o2, out)
+        o3, i3, _ = run(cfg, other, moe2, cuda)
+        np.testing.assert_array_equal(o3, want2["output"])
+
 
 
 @pytest.mark.parametrize("cfg_index,check", [(0, None), (2, 12), (3, 6)])
