@@ -55,9 +55,19 @@ typedef enum {
      * CPU oracle, to the per-matrix k3_rocm_mxfp4_* entry points and
      * between decode and any batch size. */
     K3_MOE_EXACT = 0,
-    /* Grouped GEMM on CDNA4 scaled MFMA: weights stay MXFP4, activations are
-     * quantised to MXFP8 (e4m3 + one E8M0 scale per 32 values). */
-    K3_MOE_MX8 = 1,
+    /* Grouped GEMM on CDNA4 scaled MFMA for token_count > 1: weights stay
+     * MXFP4; each bf16 activation enters as two MXFP8 terms hi + lo (E4M3
+     * codes, one E8M0 scale per 32 values), which reproduce it exactly
+     * except for elements more than 2^6 below their block maximum (error
+     * <= 2^-22 of it). Products are those of the bf16 inputs; accumulation
+     * is fp32 in MFMA order, so results match EXACT within bf16 tolerance,
+     * not bit for bit. One token runs the EXACT decode path. */
+    K3_MOE_MFMA = 1,
+    /* As K3_MOE_MFMA with one MXFP8 term (half the MFMA work). Activation
+     * quantisation error is ~4% per element and survives the dot products
+     * (~5% relative on expert outputs): an approximate mode, not a
+     * drop-in for the reference's numerics. */
+    K3_MOE_MFMA_FP8 = 2,
 } k3_moe_precision;
 
 typedef struct {
@@ -165,6 +175,20 @@ bool k3_moe_experts_bf16(void *output, const void *hidden, const void *residual,
                          const k3_moe_shape *shape, uint32_t token_count,
                          uint32_t precision, void *workspace,
                          size_t workspace_bytes, void *stream);
+
+/*
+ * MXFP8 quantisation of `count` bf16 values (count % 32 == 0; src and the
+ * code arrays 16-byte aligned) as the MFMA precisions feed activations:
+ * per block of 32, X = floor(log2(max |x|)) - 8 (+1 if the maximum would
+ * exceed 448 after scaling; >= -127), scale byte X + 127, codes E4M3(x *
+ * 2^-X) rounded to nearest even. With lo_codes/lo_scales non-NULL the
+ * residual x - hi is quantised the same way (the two-term split of
+ * K3_MOE_MFMA). No reference counterpart: exported so callers and tests
+ * can check the activation encoding on its own.
+ */
+bool k3_moe_mx8_quantize_bf16(uint8_t *hi_codes, uint8_t *hi_scales, uint8_t *lo_codes,
+                              uint8_t *lo_scales, const void *src, uint64_t count,
+                              void *stream);
 
 /*
  * Synthetic resident expert store for benchmarks and tests: fills `bytes`

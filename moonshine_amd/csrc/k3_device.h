@@ -215,4 +215,58 @@ __device__ __forceinline__ int wave_rows_owner() {
     return row;
 }
 
+/* ---- MXFP8 (E4M3 codes + E8M0 block scales) ------------------------------ */
+
+/* floor(log2(a)) of a finite a > 0 (normal or subnormal). */
+__device__ __forceinline__ int ilog2_pos(float a) {
+    const uint32_t u = __float_as_uint(a);
+    const int e = (int)((u >> 23) & 255u);
+    if (e) return e - 127;
+    return (31 - __clz((int)(u & 0x7fffffu))) - 149;
+}
+
+/* OCP E4M3 decode (bias 7, subnormal step 2^-9, S.1111.111 = NaN). */
+__device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
+    const uint32_t e = (v >> 3) & 15u, m = v & 7u;
+    float mag;
+    if (e == 15u && m == 7u) mag = __uint_as_float(0x7fc00000u);
+    else if (e) mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    else mag = __fmul_rn((float)m, 0.001953125f);
+    return (v & 0x80u) ? -mag : mag;
+}
+
+/* fp32 -> E4M3, round to nearest even, magnitude clamped to 448, NaN ->
+ * 0x7f (the same steps as the CPU oracle's conversion). */
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+    if (v != v) return 0x7fu;
+    const uint32_t sign = (__float_as_uint(v) >> 31) << 7;
+    float a = fabsf(v);
+    if (a > 448.0f) a = 448.0f;
+    if (a < 0.015625f) return sign | (uint32_t)rintf(__fmul_rn(a, 512.0f));
+    const int e = (int)((__float_as_uint(a) >> 23) & 255u) - 127;
+    const float m = __fmul_rn(a, __uint_as_float((uint32_t)(127 - e) << 23));
+    int mant = (int)rintf(__fmul_rn(__fsub_rn(m, 1.0f), 8.0f));
+    int ee = e;
+    if (mant == 8) { mant = 0; ee++; }
+    return sign | (uint32_t)(((ee + 7) << 3) | mant);
+}
+
+/* Block exponent for MXFP8: floor(log2(amax)) - 8, plus one when the
+ * maximum would exceed 448 after scaling, clamped to >= -127; -127 for an
+ * all-zero block. Returns the scale byte (X + 127). */
+__device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
+    int X = -127;
+    if (amax > 0.0f) {
+        X = ilog2_pos(amax) - 8;
+        if (__fmul_rn(amax, __uint_as_float((uint32_t)(127 - X) << 23)) > 448.0f) X++;
+        if (X < -127) X = -127;
+    }
+    return (uint32_t)(X + 127);
+}
+
+/* 2^-(byte - 127) as the multiplier applied before rounding to E4M3. */
+__device__ __forceinline__ float mx8_inv_scale(uint32_t byte) {
+    return __uint_as_float((254u - byte) << 23);
+}
+
 }  // namespace k3

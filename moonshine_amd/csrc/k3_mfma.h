@@ -1,0 +1,45 @@
+/*
+ * Grouped expert products on CDNA4 scaled MFMA (prefill / batched tokens).
+ *
+ * Activations enter the MFMA as MXFP8 (E4M3 codes, one E8M0 scale per 32
+ * along K) against the experts' native MXFP4 weights, through
+ * V_MFMA_SCALE_F32_16X16X128_F8F6F4. In the split precision every bf16
+ * activation is carried as two MXFP8 terms hi + lo (lo quantizes x - hi),
+ * which reproduces it exactly except for elements more than 2^6 below their
+ * block maximum (error <= 2^-22 of that maximum), so the products are those
+ * of the bf16 inputs and only the fp32 accumulation order differs from the
+ * exact path.
+ */
+#pragma once
+
+#include "k3_decode.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "k3_moe.h"
+
+namespace k3 {
+
+struct MfmaBuffers {
+    uint8_t *xq[2], *xs[2];     /* [T, H] codes, [T, H / 32] scales: hi, lo */
+    uint8_t *aq[2], *as[2];     /* [routes, F] codes, [routes, F / 32] scales */
+    uint32_t *tiles;            /* 3 classes x tile_cap x {expert, row0, rows} */
+    uint32_t *tile_count;       /* [4] */
+    uint32_t tile_cap[3];
+};
+
+/* Device tile bounds for T tokens (per class: 16-, 32- and 64-row tiles). */
+void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[3]);
+
+/* Plan (counts/offsets/unique/token_index/route_index) must be on the
+ * stream already. Writes y [routes, H] bf16 in route order. terms: 1 or 2. */
+bool mfma_supported(const k3_moe_shape &s);
+
+bool mfma_launch_experts(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
+                         const uint32_t *counts, const uint32_t *offsets,
+                         const uint32_t *token_index, const uint32_t *route_index,
+                         const k3_moe_expert *experts, const k3_moe_shape &s, uint32_t T,
+                         uint32_t terms, hipStream_t st, const StageMarker &mark);
+
+}  // namespace k3

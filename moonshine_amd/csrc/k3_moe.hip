@@ -12,7 +12,9 @@
  *   T  > 1: device routing plan (count -> scan -> stable scatter), then
  *           grouped gate/up and down over the selected experts only (each
  *           expert's weights are read once per row block for all its
- *           tokens), then the slotted combine.
+ *           tokens), then the slotted combine. K3_MOE_EXACT runs the w64
+ *           VALU kernels below; K3_MOE_MFMA / _FP8 the scaled-MFMA tiles
+ *           of k3_mfma.hip.
  *
  * No host synchronisation anywhere: the expert ids never leave the device.
  * Every product uses the per-row w64 order of k3_ops.hip, so the decode and
@@ -21,6 +23,7 @@
 #include "k3_device.h"
 #include "k3_internal.h"
 #include "k3_decode.h"
+#include "k3_mfma.h"
 #include "../../include/k3_moe.h"
 #include "../../include/k3_rocm_ops.h"
 
@@ -52,6 +55,7 @@ struct Workspace {
     uint16_t *act;
     k3_moe_expert *sel;
     uint16_t *y;
+    MfmaBuffers mfma;
     size_t bytes;
 };
 
@@ -83,7 +87,24 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
     w.chunk_base = (uint32_t *)take(plan_scratch(T, s.expert_count));
     w.act = (uint16_t *)take(2ull * routes * s.ffn);
     w.sel = (k3_moe_expert *)take(T == 1u ? sizeof(k3_moe_expert) * s.top_k : 0u);
-    w.y = (uint16_t *)take(T > 1u ? 2ull * routes * s.hidden : 0u);
+    /* grouped path: every T > 1, and T == 1 when the decode kernels do not
+     * cover the shape */
+    const bool grouped = T > 1u || !decode_supported(s);
+    w.y = (uint16_t *)take(grouped ? 2ull * routes * s.hidden : 0u);
+    if (grouped) {
+        /* MFMA path: activation codes reuse `act` (two byte planes of the
+         * bf16 activation's size) */
+        MfmaBuffers &m = w.mfma;
+        for (int t = 0; t < 2; t++) {
+            m.xq[t] = take(1ull * T * s.hidden);
+            m.xs[t] = take(1ull * T * s.hidden / 32u);
+            m.aq[t] = w.act ? (uint8_t *)w.act + (uint64_t)t * routes * s.ffn : nullptr;
+            m.as[t] = take(1ull * routes * s.ffn / 32u);
+        }
+        mfma_tile_caps(T, s.top_k, s.expert_count, m.tile_cap);
+        m.tiles = (uint32_t *)take(12ull * (m.tile_cap[0] + m.tile_cap[1] + m.tile_cap[2]));
+        m.tile_count = (uint32_t *)take(16u);
+    }
     w.bytes = off;
     return w;
 }
@@ -387,6 +408,14 @@ bool shape_ok(const k3_moe_shape *s) {
            (s->activation == 1u || (s->beta > 0.0f && s->linear_beta > 0.0f));
 }
 
+/* precision and shape checks shared by the layer entry points; the MFMA
+ * precisions need H % 256 == 0 and F % 128 == 0 when T > 1 */
+bool precision_ok(const k3_moe_shape *s, uint32_t T, uint32_t precision) {
+    if (!shape_ok(s) || T == 0u || T > 65535u || precision > K3_MOE_MFMA_FP8) return false;
+    if (precision != K3_MOE_EXACT && T > 1u && !mfma_supported(*s)) return false;
+    return true;
+}
+
 DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden,
                            const void *residual, const void *router_weight,
                            const void *router_bias, const k3_moe_expert *experts,
@@ -421,11 +450,11 @@ DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden
 /* Expert stage on routes already in ws.ids / ws.weights. */
 bool run_experts(const Workspace &ws, void *output, const void *hidden, const void *residual,
                  const k3_moe_expert *experts, const k3_moe_shape &s, uint32_t T,
-                 hipStream_t st, const StageMarker &mark) {
+                 uint32_t precision, hipStream_t st, const StageMarker &mark) {
     const uint32_t H = s.hidden, F = s.ffn, E = s.expert_count, k = s.top_k;
     const float beta = s.activation == 1u ? 1.0f : s.beta;
     const float lb = s.activation == 1u ? 1.0f : s.linear_beta;
-    if (T == 1u && decode_supported(s)) {
+    if (T == 1u && decode_supported(s)) { /* every precision: exact decode */
         const DecodeParams P = decode_params(ws, output, hidden, residual, nullptr, nullptr,
                                              experts, s, nullptr, nullptr);
         return decode_launch_experts(P, st, mark, true);
@@ -434,6 +463,18 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
     if (!launch_plan(ws.counts, ws.offsets, ws.unique, ws.summary, ws.token_index,
                      ws.route_index, ws.chunk_base, ws.ids, T, k, E, st))
         return false;
+    if (precision != K3_MOE_EXACT) {
+        if (!mfma_launch_experts(ws.mfma, ws.y, (const uint16_t *)hidden, ws.counts, ws.offsets,
+                                 ws.token_index, ws.route_index, experts, s, T,
+                                 precision == K3_MOE_MFMA ? 2u : 1u, st, mark))
+            return false;
+        mark(K3_MOE_STAGE_COMBINE);
+        hipLaunchKernelGGL(combine_kernel, dim3((H + 255u) / 256u, T), dim3(256), 0, st,
+                           (uint16_t *)output, ws.y, (const uint16_t *)residual, ws.ids,
+                           ws.weights, H, k, E);
+        mark(K3_MOE_STAGE_END);
+        return hipGetLastError() == hipSuccess;
+    }
     const uint32_t upper = (uint64_t)T * k < E ? T * k : E;
     constexpr int RW = 4, TT = 4, RB = 4;
     mark(K3_MOE_STAGE_GATE_UP);
@@ -495,7 +536,7 @@ extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void
                                     uint32_t token_count, uint32_t precision, void *workspace,
                                     size_t workspace_bytes, void *stream) {
     if (!output || !hidden || !expert_ids || !expert_weights || !experts || !workspace ||
-        !shape_ok(shape) || token_count == 0u || token_count > 65535u || precision != K3_MOE_EXACT)
+        !precision_ok(shape, token_count, precision))
         return false;
     Workspace ws = carve(workspace, *shape, token_count);
     if (workspace_bytes < ws.bytes) return false;
@@ -505,7 +546,7 @@ extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void
         hipMemcpyAsync(ws.weights, expert_weights, route_bytes, hipMemcpyDeviceToDevice, st) !=
             hipSuccess)
         return false;
-    return run_experts(ws, output, hidden, residual, experts, *shape, token_count, st,
+    return run_experts(ws, output, hidden, residual, experts, *shape, token_count, precision, st,
                        StageMarker{nullptr, st});
 }
 
@@ -517,8 +558,7 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
                                     size_t workspace_bytes, const k3_moe_profile *profile,
                                     void *stream) {
     if (!output || !hidden || !router_weight || !router_bias || !experts || !workspace ||
-        !shape_ok(shape) || token_count == 0u || token_count > 65535u || precision != K3_MOE_EXACT ||
-        ((uintptr_t)hidden % 16u) != 0u)
+        !precision_ok(shape, token_count, precision) || ((uintptr_t)hidden % 16u) != 0u)
         return false;
     Workspace ws = carve(workspace, *shape, token_count);
     if (workspace_bytes < ws.bytes) return false;
@@ -538,7 +578,8 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
                             ws.logits, (const float *)router_bias, token_count,
                             shape->expert_count, shape->top_k, shape->scaling_factor, st))
         return false;
-    return run_experts(ws, output, hidden, residual, experts, *shape, token_count, st, mark);
+    return run_experts(ws, output, hidden, residual, experts, *shape, token_count, precision, st,
+                       mark);
 }
 
 extern "C" bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,

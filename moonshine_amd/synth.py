@@ -10,7 +10,8 @@ from dataclasses import dataclass
 import numpy as np
 
 EXACT = 0
-MX8 = 1
+MFMA = 1      # two-term MXFP8 activations on scaled MFMA (bf16 tolerance)
+MFMA_FP8 = 2  # one-term MXFP8 activations (approximate)
 ACT_SITU = 0
 ACT_SWIGLU = 1
 

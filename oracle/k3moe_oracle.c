@@ -375,6 +375,116 @@ static double mx_row_f64(const uint8_t *p, const uint8_t *s,
     return acc;
 }
 
+/* ---- MX8 activations (MXFP8: OCP E4M3 codes + one E8M0 scale per 32) ---- */
+
+/* OCP E4M3 ("fn") decode: bias 7, no infinities, S.1111.111 = NaN. */
+float k3o_e4m3(uint8_t v) {
+    const uint32_t e = (v >> 3) & 15u, m = v & 7u;
+    if (e == 15u && m == 7u) return u2f(0x7fc00000u);
+    const float mag = e ? ldexpf(1.0f + (float)m / 8.0f, (int)e - 7)
+                        : ldexpf((float)m / 8.0f, -6);
+    return (v & 0x80u) ? -mag : mag;
+}
+
+/* fp32 -> E4M3, round to nearest even, magnitude clamped to 448 (the
+ * largest finite code), NaN -> 0x7f. Built from the value's own exponent so
+ * host and device evaluate the same steps. */
+uint8_t k3o_f32_to_e4m3(float v) {
+    if (v != v) return 0x7fu;
+    const uint8_t sign = (f2u(v) >> 31) ? 0x80u : 0u;
+    float a = fabsf(v);
+    if (a > 448.0f) a = 448.0f;
+    if (a < 0.015625f) /* below 2^-6: subnormal step 2^-9 (code 8 = 2^-6) */
+        return sign | (uint8_t)rintf(a * 512.0f);
+    const int e = (int)((f2u(a) >> 23) & 255u) - 127; /* a is a normal fp32 */
+    const float m = a * u2f((uint32_t)(127 - e) << 23);  /* [1, 2) exactly */
+    int mant = (int)rintf((m - 1.0f) * 8.0f);
+    int ee = e;
+    if (mant == 8) { mant = 0; ee++; }
+    return sign | (uint8_t)(((ee + 7) << 3) | mant);
+}
+
+/* floor(log2(a)) of a finite a > 0 (normal or subnormal fp32). */
+static int ilog2f_pos(float a) {
+    const uint32_t u = f2u(a);
+    const int e = (int)((u >> 23) & 255u);
+    if (e) return e - 127;
+    return (31 - __builtin_clz(u & 0x7fffffu)) - 149;
+}
+
+/* MXFP8 quantization of one block of 32 fp32 values: X = floor(log2(max
+ * |v|)) - 8, plus one when max |v| * 2^-X exceeds 448 (E4M3's largest
+ * finite value, so nothing saturates), clamped to >= -127 (X = -127 for an
+ * all-zero block); scale byte = X + 127, q = E4M3(v * 2^-X) rounded to
+ * nearest even. The scaled maximum lands in (224, 448]. */
+static void mx8_block(uint8_t *q, uint8_t *scale, const float *v) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        const float a = fabsf(v[i]);
+        amax = a > amax ? a : amax;
+    }
+    int X = -127;
+    if (amax > 0.0f) {
+        X = ilog2f_pos(amax) - 8;
+        if (amax * u2f((uint32_t)(127 - X) << 23) > 448.0f) X++;
+        if (X < -127) X = -127;
+    }
+    *scale = (uint8_t)(X + 127);
+    const float inv = X == -127 ? u2f(0x7f000000u) : u2f((uint32_t)(127 - X) << 23);
+    for (int i = 0; i < 32; i++) q[i] = k3o_f32_to_e4m3(v[i] * inv);
+}
+
+static float mx8_value(uint8_t q, uint8_t scale) {
+    return k3o_e4m3(q) * k3o_e8m0(scale);
+}
+
+void k3o_mx8_quantize(uint8_t *q, uint8_t *scales, const uint16_t *src, uint64_t n) {
+    float v[32];
+    for (uint64_t b = 0; b < n / 32u; b++) {
+        for (int i = 0; i < 32; i++) v[i] = k3o_bf16_to_f32(src[32u * b + i]);
+        mx8_block(q + 32u * b, scales + b, v);
+    }
+}
+
+/* Two-term MXFP8 split: hi = MXFP8(x), lo = MXFP8(x - hi) with its own
+ * block scale (the difference is exact in fp32). hi + lo reproduces every
+ * bf16 element whose exponent is within 2^-6 of its block maximum exactly,
+ * and smaller ones to within 2^-22 of the block maximum. */
+void k3o_mx8_split(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
+                   const uint16_t *src, uint64_t n) {
+    float v[32], r[32];
+    for (uint64_t b = 0; b < n / 32u; b++) {
+        for (int i = 0; i < 32; i++) v[i] = k3o_bf16_to_f32(src[32u * b + i]);
+        mx8_block(hi_q + 32u * b, hi_s + b, v);
+        for (int i = 0; i < 32; i++) r[i] = v[i] - mx8_value(hi_q[32u * b + i], hi_s[b]);
+        mx8_block(lo_q + 32u * b, lo_s + b, r);
+    }
+}
+
+/* bf16 bits of the split's reconstruction hi + lo, rounded to bf16 (it is
+ * exactly x for every element that matters; used only to feed fp64). */
+static double mx_row_split(const uint8_t *p, const uint8_t *s, const uint8_t *hq,
+                           const uint8_t *hs, const uint8_t *lq, const uint8_t *ls,
+                           uint32_t cols) {
+    double acc = 0.0;
+    for (uint32_t c = 0; c < cols; c++) {
+        const double xv = (double)mx8_value(hq[c], hs[c / 32u]) +
+                          (double)mx8_value(lq[c], ls[c / 32u]);
+        acc += (double)nib(p, c) * (double)k3o_e8m0(s[c / 32u]) * xv;
+    }
+    return acc;
+}
+
+/* fp64 dot of one MXFP4 row with MXFP8-quantized activations. */
+static double mx_row_mx8(const uint8_t *p, const uint8_t *s, const uint8_t *xq,
+                         const uint8_t *xs, uint32_t cols) {
+    double acc = 0.0;
+    for (uint32_t c = 0; c < cols; c++)
+        acc += (double)nib(p, c) * (double)k3o_e8m0(s[c / 32u]) *
+               (double)k3o_e4m3(xq[c]) * (double)k3o_e8m0(xs[c / 32u]);
+    return acc;
+}
+
 void k3o_mxfp4_gemm(uint16_t *out, float *out_f32, const uint8_t *packed,
                     const uint8_t *scales, const uint16_t *input,
                     uint32_t vectors, uint32_t rows, uint32_t columns,
@@ -502,6 +612,16 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
         uint16_t *g = (uint16_t *)malloc(2u * F), *u = (uint16_t *)malloc(2u * F);
         uint16_t *a = (uint16_t *)malloc(2u * F);
         const int ord = gemv_order;
+        uint8_t *xq = NULL, *xs = NULL, *aq = NULL, *as = NULL;
+        uint8_t *xq2 = NULL, *xs2 = NULL, *aq2 = NULL, *as2 = NULL;
+        if (ord == 3 || ord == 4) {
+            xq = (uint8_t *)malloc(H); xs = (uint8_t *)malloc(H / 32u);
+            aq = (uint8_t *)malloc(F); as = (uint8_t *)malloc(F / 32u);
+            xq2 = (uint8_t *)malloc(H); xs2 = (uint8_t *)malloc(H / 32u);
+            aq2 = (uint8_t *)malloc(F); as2 = (uint8_t *)malloc(F / 32u);
+            if (ord == 3) k3o_mx8_quantize(xq, xs, x, H);
+            else k3o_mx8_split(xq, xs, xq2, xs2, x, H);
+        }
         for (uint32_t row = 0; row < F; row++) {
             const uint64_t po = (uint64_t)row * (H / 2u), so = (uint64_t)row * (H / 32u);
             float vg, vu;
@@ -511,6 +631,12 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
             } else if (ord == 1) {
                 vg = mx_row_ref128(ex->w1_packed + po, ex->w1_scales + so, x, H);
                 vu = mx_row_ref128(ex->w3_packed + po, ex->w3_scales + so, x, H);
+            } else if (ord == 3) {
+                vg = (float)mx_row_mx8(ex->w1_packed + po, ex->w1_scales + so, xq, xs, H);
+                vu = (float)mx_row_mx8(ex->w3_packed + po, ex->w3_scales + so, xq, xs, H);
+            } else if (ord == 4) {
+                vg = (float)mx_row_split(ex->w1_packed + po, ex->w1_scales + so, xq, xs, xq2, xs2, H);
+                vu = (float)mx_row_split(ex->w3_packed + po, ex->w3_scales + so, xq, xs, xq2, xs2, H);
             } else {
                 vg = (float)mx_row_f64(ex->w1_packed + po, ex->w1_scales + so, x, H);
                 vu = (float)mx_row_f64(ex->w3_packed + po, ex->w3_scales + so, x, H);
@@ -520,16 +646,21 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
         }
         if (sh->activation == 1u) k3o_swiglu(a, g, u, F, 0);
         else k3o_situ(a, g, u, F, sh->beta, sh->linear_beta, 0);
+        if (ord == 3) k3o_mx8_quantize(aq, as, a, F);
+        if (ord == 4) k3o_mx8_split(aq, as, aq2, as2, a, F);
         uint16_t *y = ys + ((uint64_t)i * K + r) * H;
         for (uint32_t row = 0; row < H; row++) {
             const uint64_t po = (uint64_t)row * (F / 2u), so = (uint64_t)row * (F / 32u);
             float v;
             if (ord == 0) v = mx_row_w64(ex->w2_packed + po, ex->w2_scales + so, a, F);
             else if (ord == 1) v = mx_row_ref128(ex->w2_packed + po, ex->w2_scales + so, a, F);
+            else if (ord == 3) v = (float)mx_row_mx8(ex->w2_packed + po, ex->w2_scales + so, aq, as, F);
+            else if (ord == 4) v = (float)mx_row_split(ex->w2_packed + po, ex->w2_scales + so, aq, as, aq2, as2, F);
             else v = (float)mx_row_f64(ex->w2_packed + po, ex->w2_scales + so, a, F);
             y[row] = k3o_f32_to_bf16(v);
         }
-        free(g); free(u); free(a);
+        free(g); free(u); free(a); free(xq); free(xs); free(aq); free(as);
+        free(xq2); free(xs2); free(aq2); free(as2);
     }
 
     for (uint32_t i = 0; i < n; i++) {

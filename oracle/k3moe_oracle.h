@@ -27,6 +27,11 @@
  *   mxfp4 GEMV             fp64 (reference envelope bars), power-of-two KATs
  *   combine / add          sequential fp32 definition + hand-computed cases
  *   layer                  composition of the above; fp64 layer bound
+ *   E4M3 / MXFP8 quant     exhaustive decode vs the OCP closed form; every
+ *                          code round-trips; RNE at every midpoint;
+ *                          torch.float8_e4m3fn conversion on a dense sweep;
+ *                          block-scale invariants (max in [256, 512));
+ *                          split: hi + lo == x for in-range elements
  *   prefill ledger         the reference's locked constants
  *                          (tests/test_k3_prefill_plan.c:15-26)
  */
@@ -111,6 +116,11 @@ typedef struct {
  * the router (lets a test check the expert stage on the GPU's own routes).
  * experts[e] may be NULL for experts that are never selected.
  * expert_out (optional) receives [tokens, top_k, hidden] bf16 slot outputs.
+ * gemv_order: 0 = w64, 1 = reference lane order, 2 = fp64, 3 = MX8 (the
+ * expert inputs -- x for gate/up, the activation for down -- quantized to
+ * MXFP8 by k3o_mx8_quantize, products accumulated in fp64; same bf16
+ * rounding points as the other orders), 4 = split MX8 (inputs as the
+ * two-term k3o_mx8_split reconstruction hi + lo, fp64 accumulation).
  * Returns 0 on success, -1 when a selected expert has no weights.
  */
 int k3o_layer(const k3o_shape *shape, uint32_t tokens,
@@ -122,6 +132,13 @@ int k3o_layer(const k3o_shape *shape, uint32_t tokens,
               uint16_t *output, uint32_t *ids_out, float *weights_out,
               float *logits_out, uint16_t *expert_out, int gemv_order,
               int threads);
+
+/* ---- MX8 activations (precision mode of the MFMA prefill path) ---------- */
+float   k3o_e4m3(uint8_t code);
+uint8_t k3o_f32_to_e4m3(float v);
+void    k3o_mx8_quantize(uint8_t *q, uint8_t *scales, const uint16_t *src, uint64_t n);
+void    k3o_mx8_split(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
+                      const uint16_t *src, uint64_t n);
 
 /* ---- prefill byte ledger (k3_prefill.c:136-234, 236-446) ---------------- */
 typedef struct {

@@ -12,7 +12,7 @@ ORACLE = ROOT / "oracle" / "libk3moe_oracle.so"
 REF_OPS = ROOT / "oracle" / "_ref" / "libk3ref_ops.so"
 REF_PREFILL = ROOT / "oracle" / "_ref" / "libk3ref_prefill.so"
 
-ORDER_W64, ORDER_REF, ORDER_F64 = 0, 1, 2
+ORDER_W64, ORDER_REF, ORDER_F64, ORDER_MX8, ORDER_SPLIT = 0, 1, 2, 3, 4
 
 _p = ctypes.c_void_p
 _u32 = ctypes.c_uint32
@@ -67,6 +67,10 @@ def lib():
             "k3o_layer": (_i, [ctypes.POINTER(Shape), _u32, _p, _p, _p, _p, ctypes.POINTER(Expert),
                               _p, _p, _p, _u32, _p, _p, _p, _p, _p, _i, _i]),
             "k3o_prefill_workspace": (_i, [_u32, ctypes.POINTER(Workspace)]),
+            "k3o_e4m3": (_f, [ctypes.c_uint8]),
+            "k3o_f32_to_e4m3": (ctypes.c_uint8, [_f]),
+            "k3o_mx8_quantize": (None, [_p, _p, _p, _u64]),
+            "k3o_mx8_split": (None, [_p, _p, _p, _p, _p, _u64]),
         }
         for n, (r, a) in sig.items():
             fn = getattr(L, n)
@@ -150,6 +154,42 @@ def add(a, b):
     out = np.empty_like(a)
     lib().k3o_add(_ptr(out), _ptr(a), _ptr(b), a.size)
     return out
+
+
+def e4m3_table():
+    return np.array([lib().k3o_e4m3(c) for c in range(256)], np.float32)
+
+
+def f32_to_e4m3(v):
+    v = np.asarray(v, np.float32).ravel()
+    return np.array([lib().k3o_f32_to_e4m3(float(x)) for x in v], np.uint8)
+
+
+def mx8_quantize(x_bf16):
+    """bf16 bits [..., n] (n % 32 == 0) -> (E4M3 codes, E8M0 scales per 32)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty(x.shape[:-1] + (x.shape[-1] // 32,), np.uint8)
+    lib().k3o_mx8_quantize(_ptr(q), _ptr(s), _ptr(x), x.size)
+    return q, s
+
+
+def mx8_split(x_bf16):
+    """bf16 bits [..., n] -> (hi codes, hi scales, lo codes, lo scales)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    hq, lq = np.empty(x.shape, np.uint8), np.empty(x.shape, np.uint8)
+    sh = x.shape[:-1] + (x.shape[-1] // 32,)
+    hs, ls = np.empty(sh, np.uint8), np.empty(sh, np.uint8)
+    lib().k3o_mx8_split(_ptr(hq), _ptr(hs), _ptr(lq), _ptr(ls), _ptr(x), x.size)
+    return hq, hs, lq, ls
+
+
+def mx8_dequantize(q, s):
+    t = e4m3_table().astype(np.float64)
+    v = t[q].reshape(q.shape[:-1] + (q.shape[-1] // 32, 32))
+    sc = np.ldexp(1.0, s.astype(np.int64) - 127)
+    sc = np.where(s == 0, 2.0 ** -127, sc)
+    return (v * sc[..., None]).reshape(q.shape)
 
 
 def layer(cfg, inputs, experts, tokens=None, ids=None, weights=None, order=ORDER_W64,

@@ -1,0 +1,154 @@
+"""GPU parity of the scaled-MFMA expert path (K3_MOE_MFMA / K3_MOE_MFMA_FP8).
+
+- The MXFP8 activation encoding (k3_moe_mx8_quantize_bf16) is bit-exact to
+  the oracle's k3o_mx8_quantize / k3o_mx8_split.
+- Routing (ids, weights, plan) is the exact path's, so ids match bit for bit.
+- Layer outputs: the MFMA accumulation order differs from the w64 order, so
+  outputs are compared at a stated tolerance, against the oracle's fp64
+  layer on the same (split) inputs and against the GPU's own exact path on
+  every token of the K3-shape batches (T = 64, 512 and the 8192-token Zipf
+  prefill, which exercises all three tile classes).
+
+Tolerance for K3_MOE_MFMA (bf16-faithful): relative L2 <= 2e-3 of the
+layer output, and every |difference| <= 4 bf16 ulps at max(|element|,
+output RMS). Each output element is a weighted sum of k expert outputs that
+were rounded to bf16 at their own (RMS-sized) magnitude, after two more bf16
+roundings (gate/up, activation) whose boundaries the fp32 order can cross;
+so an element that cancels to near zero still carries errors of a few
+RMS-sized ulps. The bound allows that and nothing more.
+"""
+import ctypes
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from moonshine_amd import layer as L
+from moonshine_amd._lib import lib
+from moonshine_amd.synth import (CONFIGS, EXACT, MFMA, MFMA_FP8, bf16_bits_to_f32,
+                                 f32_to_bf16_bits, make_inputs)
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 2e-3
+ULPS = 4
+
+_stores = {}
+
+
+def get_layer(cfg, inputs, cuda):
+    key = (cfg.experts, cfg.hidden, cfg.ffn, cfg.seed)
+    if key not in _stores:
+        _stores.clear()
+        torch.cuda.empty_cache()
+        _stores[key] = L.ExpertStore(cfg.experts, cfg.hidden, cfg.ffn, seed=cfg.seed, device=cuda)
+    return L.build_layer(cfg, inputs, device=cuda, store=_stores[key])
+
+
+def forward(moe, inputs, cuda, precision):
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    T, k = x.shape[0], moe.shape.top_k
+    ids = torch.zeros((T, k), dtype=torch.int32, device=cuda)
+    w = torch.zeros((T, k), dtype=torch.float32, device=cuda)
+    out = moe.forward(x, r, ids=ids, weights=w, precision=precision)
+    torch.cuda.synchronize()
+    return L.bf16_bits(out), ids.cpu().numpy().view(np.uint32), w.cpu().numpy()
+
+
+def assert_close(got_bits, want_bits, what):
+    got = bf16_bits_to_f32(got_bits).astype(np.float64)
+    want = bf16_bits_to_f32(want_bits).astype(np.float64)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    rms = np.sqrt(np.mean(want ** 2))
+    # bf16 ulp at max(|element|, rms)
+    ulp = np.ldexp(1.0, np.frexp(np.maximum(np.abs(want), rms))[1] - 8)
+    d = np.abs(got - want)
+    worst = (d / ulp).max()
+    print(f"{what}: rel-L2 {rel:.3g}, max |d| {d.max():.4g}, worst {worst:.2f} ulp "
+          f"(rms {rms:.4g}), elements differing {np.mean(got != want):.3%}")
+    assert rel <= REL_L2, f"{what}: relative L2 {rel:.3g} > {REL_L2}"
+    assert worst <= ULPS, f"{what}: an element differs by {worst:.2f} > {ULPS} ulp"
+
+
+def test_mx8_quantize_bitexact(cuda):
+    rng = np.random.default_rng(21)
+    n = 32 * 4096
+    x = rng.standard_normal(n).astype(np.float32) * np.repeat(
+        np.ldexp(1.0, rng.integers(-60, 60, n // 32)), 32)
+    x[:32] = 0.0
+    x[32:64] = 1e-39
+    x[64:96] = np.float32(6.5e4) * rng.standard_normal(32).astype(np.float32)
+    xb = f32_to_bf16_bits(x)
+    src = torch.from_numpy(xb.view(np.int16)).to(cuda)
+    hq = torch.empty(n, dtype=torch.uint8, device=cuda)
+    lq = torch.empty(n, dtype=torch.uint8, device=cuda)
+    hs = torch.empty(n // 32, dtype=torch.uint8, device=cuda)
+    ls = torch.empty(n // 32, dtype=torch.uint8, device=cuda)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib().k3_moe_mx8_quantize_bf16(P(hq), P(hs), P(lq), P(ls), P(src), n, st)
+    torch.cuda.synchronize()
+    want = O.mx8_split(xb)
+    for got, exp in zip((hq, hs, lq, ls), want):
+        np.testing.assert_array_equal(got.cpu().numpy(), exp)
+    assert lib().k3_moe_mx8_quantize_bf16(P(hq), P(hs), None, None, P(src), n, st)
+    torch.cuda.synchronize()
+    q1, s1 = O.mx8_quantize(xb)
+    np.testing.assert_array_equal(hq.cpu().numpy(), q1)
+    np.testing.assert_array_equal(hs.cpu().numpy(), s1)
+    # argument checks
+    assert not lib().k3_moe_mx8_quantize_bf16(P(hq), P(hs), None, None, P(src), 33, st)
+    assert not lib().k3_moe_mx8_quantize_bf16(P(hq), P(hs), P(lq), None, P(src), n, st)
+
+
+def small_cfg(tokens):
+    """Config 0's shape (H 2048, 64 experts, top-4, F 512) with a batch."""
+    return dataclasses.replace(CONFIGS[0], name=f"cfg0x{tokens}", tokens=tokens)
+
+
+@pytest.mark.parametrize("precision,order", [(MFMA, O.ORDER_SPLIT), (MFMA_FP8, O.ORDER_MX8)],
+                         ids=["mfma", "mfma_fp8"])
+def test_small_batch_vs_oracle(cuda, precision, order):
+    cfg = small_cfg(72)
+    inputs = make_inputs(cfg, tokens=cfg.tokens)
+    moe = get_layer(cfg, inputs, cuda)
+    out, ids, w = forward(moe, inputs, cuda, precision)
+    want_ids, want_w = O.router_topk(O.router_logits(inputs.router_weight, inputs.hidden),
+                                     inputs.router_bias, cfg.top_k, cfg.scale)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(w, want_w)
+    experts = {int(e): moe.store.host_expert(int(e)) for e in np.unique(ids)}
+    want = O.layer(cfg, inputs, experts, order=order)
+    assert_close(out, want["output"], f"precision {precision} vs oracle order {order}")
+    if precision == MFMA:
+        exact, _, _ = forward(moe, inputs, cuda, EXACT)
+        assert_close(out, exact, "mfma vs exact (GPU)")
+
+
+@pytest.mark.parametrize("cfg_index", [2, 3, 4])
+def test_k3_batches_vs_exact(cuda, cfg_index):
+    cfg = CONFIGS[cfg_index]
+    inputs = make_inputs(cfg, tokens=cfg.tokens)
+    moe = get_layer(cfg, inputs, cuda)
+    print(f"{cfg.name}: T={cfg.tokens}", flush=True)
+    out, ids, w = forward(moe, inputs, cuda, MFMA)
+    exact, ids_e, w_e = forward(moe, inputs, cuda, EXACT)
+    np.testing.assert_array_equal(ids, ids_e)
+    np.testing.assert_array_equal(w, w_e)
+    assert_close(out, exact, f"{cfg.name} mfma vs exact")
+    # repeat: same bits (no state carried between calls)
+    again, _, _ = forward(moe, inputs, cuda, MFMA)
+    np.testing.assert_array_equal(again, out)
+
+
+def test_unsupported_shape_rejected(cuda):
+    cfg = dataclasses.replace(CONFIGS[0], name="odd", tokens=4, hidden=2080, experts=16, top_k=2,
+                              seed=3)
+    inputs = make_inputs(cfg, tokens=4)
+    moe = L.build_layer(cfg, inputs, device=cuda)
+    with pytest.raises(RuntimeError):
+        forward(moe, inputs, cuda, MFMA)
+    forward(moe, inputs, cuda, EXACT)  # the exact path takes any H % 32 == 0

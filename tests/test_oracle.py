@@ -214,3 +214,142 @@ def test_prefill_workspace_ledger_reference_constants():
         assert w.batch_workspace_bytes == 1116360 * chunk
         assert w.incremental_workspace_bytes == 1116360 * (chunk - 1)
         assert w.mla_append_bytes == chunk * 24 * 576 * 2
+
+
+def _e4m3_closed_form(code):
+    """OCP E4M3 ("fn"): bias 7, subnormals m/8 * 2^-6, S.1111.111 = NaN."""
+    s, e, m = code >> 7, (code >> 3) & 15, code & 7
+    if e == 15 and m == 7:
+        return math.nan
+    mag = (1 + m / 8) * 2.0 ** (e - 7) if e else (m / 8) * 2.0 ** -6
+    return -mag if s else mag
+
+
+def test_e4m3_decode_exhaustive_vs_closed_form_and_torch():
+    table = O.e4m3_table()
+    want = np.array([_e4m3_closed_form(c) for c in range(256)], np.float32)
+    np.testing.assert_array_equal(np.isnan(table), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(table[ok], want[ok])
+    tt = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(table[ok], tt[ok])
+    assert table[0x7E] == 448.0 and table[0x08] == 2.0 ** -6 and table[0x01] == 2.0 ** -9
+
+
+def test_f32_to_e4m3_round_trip_rne_and_torch():
+    table = O.e4m3_table()
+    codes = np.array([c for c in range(256) if not np.isnan(table[c])], np.uint8)
+    # every finite code round-trips (-0 keeps its sign bit)
+    np.testing.assert_array_equal(O.f32_to_e4m3(table[codes]), codes)
+    # midpoints between neighbouring positive codes round to the even code
+    pos = np.sort(table[codes[codes < 0x80]].astype(np.float64))
+    mids = (pos[:-1] + pos[1:]) / 2
+    got = table[O.f32_to_e4m3(mids.astype(np.float32))].astype(np.float64)
+    lo_code = O.f32_to_e4m3(pos[:-1].astype(np.float32))
+    hi_code = O.f32_to_e4m3(pos[1:].astype(np.float32))
+    even = np.where(lo_code % 2 == 0, pos[:-1], pos[1:])
+    assert np.all((hi_code - lo_code) == 1)
+    np.testing.assert_array_equal(got, even)
+    # dense sweep against torch's float8_e4m3fn cast (RNE) inside the range
+    rng = np.random.default_rng(7)
+    v = np.concatenate([rng.uniform(-448, 448, 20000), rng.uniform(-0.02, 0.02, 20000),
+                        np.ldexp(rng.uniform(1, 2, 20000), rng.integers(-12, 9, 20000))])
+    v = np.clip(v, -448, 448).astype(np.float32)  # torch's cast gives NaN beyond
+    want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(O.f32_to_e4m3(v), want)
+    # saturation and NaN
+    assert O.f32_to_e4m3([1e6])[0] == 0x7E and O.f32_to_e4m3([-500.0])[0] == 0xFE
+    assert O.f32_to_e4m3([math.nan])[0] == 0x7F
+
+
+def test_mx8_quantize_block_invariants_and_torch():
+    rng = np.random.default_rng(11)
+    n_blocks = 4096
+    mag = np.ldexp(1.0, rng.integers(-40, 40, n_blocks))[:, None]
+    x = (rng.standard_normal((n_blocks, 32)) * mag).astype(np.float32)
+    x[5] = 0.0                      # all-zero block
+    x[6, 3] = 1e-39                 # fp32-subnormal maximum elsewhere tiny
+    x[6, np.arange(32) != 3] = 0.0
+    xb = f32_to_bf16_bits(x)
+    xf = bf16_bits_to_f32(xb).astype(np.float64)
+    q, s2 = O.mx8_quantize(xb)
+    s = s2[:, 0]
+    X = s.astype(np.int64) - 127
+    amax = np.abs(xf).max(axis=1)
+    nz = (amax > 0) & (X > -127)
+    # the block maximum lands in (224, 448]: E4M3's top binade, or the one
+    # below when the top one would saturate
+    r = amax[nz] * np.ldexp(1.0, -X[nz])
+    assert np.all((r > 224) & (r <= 448))
+    assert np.all((r >= 256) | (amax[nz] * np.ldexp(1.0, -X[nz] + 1) > 448))
+    assert X[6] == -127  # a maximum below 2^-119 is clamped to the smallest scale
+    assert s[5] == 0 and np.all(q[5] == 0)
+    # codes are torch's RNE cast of x * 2^-X, clamped to the finite range
+    scaled = np.clip(xf * np.ldexp(1.0, -X)[:, None], -448, 448).astype(np.float32)
+    want = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(q, want)
+    # dequantized error: <= half an E4M3 step of the block's top binade
+    deq = O.mx8_dequantize(q, s2)
+    step = np.ldexp(1.0, X + 8 - 3)[:, None]
+    assert np.all(np.abs(deq - xf) <= step / 2)
+
+
+def test_mx8_layer_close_to_exact_layer():
+    cfg = CONFIGS[0]
+    inputs = make_inputs(cfg)
+    rng = np.random.default_rng(cfg.seed)
+    ids = O.router_topk(O.router_logits(inputs.router_weight, inputs.hidden), inputs.router_bias,
+                        cfg.top_k, cfg.scale)[0]
+    sizes = (cfg.ffn * cfg.hidden // 2, cfg.ffn * cfg.hidden // 32) * 3
+    experts = {}
+    for e in ids[0]:
+        experts[int(e)] = [rng.integers(0, 256, n, dtype=np.uint8) if j % 2 == 0 else
+                           rng.integers(121, 126, n, dtype=np.uint8) for j, n in enumerate(sizes)]
+    ex = O.layer(cfg, inputs, experts, order=O.ORDER_F64)
+    mx = O.layer(cfg, inputs, experts, order=O.ORDER_MX8)
+    np.testing.assert_array_equal(ex["ids"], mx["ids"])
+    ye = bf16_bits_to_f32(ex["expert_out"]).astype(np.float64)
+    ym = bf16_bits_to_f32(mx["expert_out"]).astype(np.float64)
+    # one-term MXFP8 activations: ~3-4% relative error per element, and a
+    # dot product of random terms keeps that relative error (5.5% here), so
+    # this mode is far outside a bf16 tolerance
+    rel = np.linalg.norm(ym - ye) / np.linalg.norm(ye)
+    assert 0.01 < rel < 0.08
+    assert not np.array_equal(ym, ye)
+
+
+def test_mx8_split_reconstructs_bf16():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((2048, 64)).astype(np.float32) * np.ldexp(1.0, rng.integers(
+        -30, 30, (2048, 1)))
+    x[3, :32] = 0.0
+    xb = f32_to_bf16_bits(x)
+    xf = bf16_bits_to_f32(xb).astype(np.float64)
+    hq, hs, lq, ls = O.mx8_split(xb)
+    rec = O.mx8_dequantize(hq, hs) + O.mx8_dequantize(lq, ls)
+    blocks = np.abs(xf).reshape(2048, 2, 32).max(axis=2)
+    top = np.repeat(blocks, 32, axis=1)
+    # exact for elements within 2^-6 of the block maximum ...
+    near = np.abs(xf) >= top * 2.0 ** -6
+    np.testing.assert_array_equal(rec[near], xf[near])
+    # ... and within 2^-22 of the block maximum for every element
+    assert np.all(np.abs(rec - xf) <= top * 2.0 ** -22)
+    assert np.all(hs[3, 0] == 0) and np.all(hq[3, :32] == 0) and np.all(lq[3, :32] == 0)
+
+
+def test_split_layer_matches_fp64_layer():
+    cfg = CONFIGS[0]
+    inputs = make_inputs(cfg)
+    rng = np.random.default_rng(cfg.seed)
+    ids = O.router_topk(O.router_logits(inputs.router_weight, inputs.hidden), inputs.router_bias,
+                        cfg.top_k, cfg.scale)[0]
+    sizes = (cfg.ffn * cfg.hidden // 2, cfg.ffn * cfg.hidden // 32) * 3
+    experts = {}
+    for e in ids[0]:
+        experts[int(e)] = [rng.integers(0, 256, n, dtype=np.uint8) if j % 2 == 0 else
+                           rng.integers(121, 126, n, dtype=np.uint8) for j, n in enumerate(sizes)]
+    ex = O.layer(cfg, inputs, experts, order=O.ORDER_F64)
+    sp = O.layer(cfg, inputs, experts, order=O.ORDER_SPLIT)
+    ye = bf16_bits_to_f32(ex["expert_out"]).astype(np.float64)
+    ys = bf16_bits_to_f32(sp["expert_out"]).astype(np.float64)
+    assert np.linalg.norm(ys - ye) / np.linalg.norm(ye) < 1e-4
