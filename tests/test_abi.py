@@ -1,0 +1,66 @@
+"""The C ABI (CPU): libk3moe.so loads and exports every function that
+include/*.h declares, the ctypes table covers them, and the host-only entry
+points (sizes, argument validation) behave without a GPU."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from moonshine_amd import _lib
+from moonshine_amd.synth import CONFIGS
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+DECL = re.compile(r"^(?:bool|size_t|void|uint\w+_t|int)\s+\**(k3_\w+)\s*\(", re.M)
+
+
+def declared():
+    out = {}
+    for h in sorted((ROOT / "include").glob("*.h")):
+        for name in DECL.findall(h.read_text()):
+            out[name] = h.name
+    return out
+
+
+def test_headers_declare_entry_points():
+    d = declared()
+    assert "k3_moe_forward_bf16" in d and "k3_rocm_mxfp4_gemv_bf16" in d
+    assert "k3_prefill_plan_build" in d and "k3_prefill_plan_build_with_aux_workspace" in d
+    assert len(d) >= 28
+
+
+@pytest.mark.parametrize("name", sorted(declared()))
+def test_library_exports(name):
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    assert hasattr(lib, name), f"{name} ({declared()[name]}) is not exported"
+
+
+def test_ctypes_table_covers_moe_and_ops_headers():
+    missing = [n for n, h in declared().items()
+               if h in ("k3_moe.h", "k3_rocm_ops.h") and n not in _lib.SIGNATURES]
+    assert not missing, missing
+
+
+def shape(cfg):
+    return _lib.K3MoeShape(cfg.hidden, cfg.experts, cfg.top_k, cfg.ffn, cfg.scale, cfg.activation,
+                           cfg.beta, cfg.linear_beta)
+
+
+def test_workspace_sizes_and_validation():
+    L = _lib.lib()
+    s1 = L.k3_moe_workspace_bytes(ctypes.byref(shape(CONFIGS[1])), 1)
+    s4 = L.k3_moe_workspace_bytes(ctypes.byref(shape(CONFIGS[4])), 8192)
+    assert 0 < s1 < (1 << 24) and s4 > 8192 * 16 * 7168 * 2
+    assert s1 % 256 == 0 and s4 % 256 == 0
+    assert L.k3_moe_workspace_bytes(ctypes.byref(shape(CONFIGS[1])), 0) == 0
+    assert L.k3_moe_workspace_bytes(ctypes.byref(shape(CONFIGS[1])), 65536) == 0
+    bad = shape(CONFIGS[1])
+    bad.top_k = 33
+    assert L.k3_moe_workspace_bytes(ctypes.byref(bad), 4) == 0
+    assert L.k3_moe_plan_scratch_bytes(8192, 896) >= 4 * 896 * 32
+    # argument checks return false before touching a device
+    assert not L.k3_moe_forward_bf16(None, None, None, None, None, None,
+                                     ctypes.byref(shape(CONFIGS[1])), 1, 0, None, None, None, 0,
+                                     None)
+    assert not L.k3_rocm_mxfp4_gemv_bf16(None, None, None, None, 16, 64, None)
+    assert not L.k3_moe_mx8_quantize_bf16(None, None, None, None, None, 32, None)
