@@ -17,8 +17,9 @@
  * Both scale operands are the E8M0 byte of K block g of the lane's row.
  * Output: lane l holds rows 4g + i (i < 4) of column c.
  *
- * Tiles: a block is 4 waves along the weight rows (each wave 4 x 16 rows)
- * sharing 16 * WM activation rows; K advances 128 per step.
+ * Tiles: a block is 4 waves over 256 weight rows and 16, 64 or 128
+ * activation rows (by the expert's row count); K advances 128 per step
+ * through a 3-stage LDS ring filled by direct-to-LDS loads.
  */
 #include "k3_device.h"
 #include "k3_mfma.h"
@@ -27,13 +28,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace k3 {
 namespace {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kTileRows[3] = {16u, 32u, 64u};
+constexpr uint32_t kTileRows[3] = {16u, 64u, 128u};
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
@@ -81,8 +85,8 @@ __global__ __launch_bounds__(256) void x_split_kernel(MfmaBuffers B, const uint1
 /* ---------------------------------------------------------------------- */
 
 /* One block of 1024 threads (thread e = expert e). Class 0: experts with
- * <= 16 rows (one 16-row tile), class 1: <= 32 rows (one 32-row tile),
- * class 2: 64-row tiles. Tiles are listed in expert order. */
+ * <= 16 rows (one 16-row tile), class 1: <= 64 rows (one 64-row tile),
+ * class 2: 128-row tiles. Tiles are listed in expert order. */
 __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
                                                           const uint32_t *__restrict__ counts,
                                                           const uint32_t *__restrict__ offsets,
@@ -90,11 +94,11 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
     __shared__ uint32_t wave_tot[3][16];
     const uint32_t e = threadIdx.x, lane = e & 63u, wave = e >> 6;
     const uint32_t n = e < E ? counts[e] : 0u;
-    const int cls = n == 0u ? 3 : (n <= 16u ? 0 : (n <= 32u ? 1 : 2));
+    const int cls = n == 0u ? 3 : (n <= 16u ? 0 : (n <= 64u ? 1 : 2));
     uint32_t nt[3], inc[3];
 #pragma unroll
     for (int c = 0; c < 3; c++) {
-        nt[c] = cls == c ? (c == 2 ? (n + 63u) / 64u : 1u) : 0u;
+        nt[c] = cls == c ? (c == 2 ? (n + 127u) / 128u : 1u) : 0u;
         inc[c] = nt[c];
     }
 #pragma unroll
@@ -130,63 +134,241 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
 }
 
 /* ---------------------------------------------------------------------- */
-/* MFMA core                                                               */
+/* MFMA core: LDS ring fed by direct-to-LDS loads                          */
 /* ---------------------------------------------------------------------- */
 
-__device__ __forceinline__ i32x8 load_fp8_frag(const uint8_t *row, uint32_t k0, uint32_t g) {
-    const uint4 a = gload((const uint4 *)(row + k0 + 16u * g));
-    const uint4 b = gload((const uint4 *)(row + k0 + 64u + 16u * g));
-    i32x8 v;
-    v[0] = (int)a.x; v[1] = (int)a.y; v[2] = (int)a.z; v[3] = (int)a.w;
-    v[4] = (int)b.x; v[5] = (int)b.y; v[6] = (int)b.z; v[7] = (int)b.w;
-    return v;
+/*
+ * Block tile: MW x NW waves; wave tile (16 WM activation rows) x (16 WN
+ * weight rows). Per K step of 128 the block stages in LDS
+ *   A   TERMS x (BM / 16) x 2 chunks of 1 KB: chunk (t, i, h) holds, in lane
+ *       order, the 16 bytes lane l supplies for half h of its FP8 fragment of
+ *       row 16 i + l % 16 (bytes 64 h + 16 (l / 16) of the step);
+ *   B   BN / 16 chunks of 1 KB: lane order FP4 fragments of 16 rows;
+ *   SA  TERMS x max(BM, 64) dwords: the 4 E8M0 bytes of each row's step;
+ *   SB  BN dwords.
+ * Every chunk is written by one global_load_lds instruction (lane l's 16 or
+ * 4 bytes land at chunk + 16 l or + 4 l), so fragments are read back with
+ * conflict-free ds_read_b128 at lane * 16. Chunks are dealt to the four
+ * waves in equal numbers per kind; the A scale chunks of small tiles (fewer
+ * than four) go to the first waves.
+ */
+template <int MW_, int NW_, int WM_, int WN_, int TERMS_, int STAGES_>
+struct TileCfg {
+    static constexpr int MW = MW_, NW = NW_, WM = WM_, WN = WN_, TERMS = TERMS_;
+    static constexpr int STAGES = STAGES_;
+    static constexpr int BM = MW * 16 * WM, BN = NW * 16 * WN;
+    static constexpr int A_CH = TERMS * (BM / 16) * 2, B_CH = BN / 16;
+    static constexpr int SA_ROWS = BM < 64 ? 64 : BM;
+    static constexpr int SA_CH = TERMS * SA_ROWS / 64, SB_CH = BN / 64;
+    static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, OFF_SA = OFF_B + B_CH * 1024;
+    static constexpr int OFF_SB = OFF_SA + SA_CH * 256, STAGE = OFF_SB + SB_CH * 256;
+    static constexpr int LDS = STAGE * STAGES;
+    static constexpr int A_PW = A_CH / 4, B_PW = B_CH / 4, SB_PW = SB_CH / 4;
+    static constexpr int SA_PW = SA_CH >= 4 ? SA_CH / 4 : 1; /* waves < SA_CH when SA_CH < 4 */
+    static constexpr int LOADS_FULL = A_PW + B_PW + SB_PW + SA_PW;
+    static constexpr int LOADS_NO_SA = A_PW + B_PW + SB_PW + (SA_CH >= 4 ? SA_PW : 0);
+    static_assert(MW * NW == 4, "four waves");
+    static_assert(A_CH % 4 == 0 && B_CH % 4 == 0 && SB_CH % 4 == 0, "chunks split evenly");
+    static_assert(SA_CH >= 4 ? SA_CH % 4 == 0 : true, "scale chunks");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int Bytes>
+__device__ __forceinline__ void dma(const uint8_t *src, uint8_t *lds) {
+    if constexpr (Bytes == 16)
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)lds, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)lds, 4, 0, 0);
 }
 
-__device__ __forceinline__ i32x8 load_fp4_frag(const uint8_t *row, uint32_t k0, uint32_t g) {
-    const uint4 a = gload((const uint4 *)(row + k0 / 2u + 16u * g));
-    i32x8 v;
-    v[0] = (int)a.x; v[1] = (int)a.y; v[2] = (int)a.z; v[3] = (int)a.w;
-    v[4] = 0; v[5] = 0; v[6] = 0; v[7] = 0;
-    return v;
+/* s_waitcnt vmcnt(N) (N < 64), other counters untouched. */
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+/* Per-lane source pointers of the chunks this wave loads. */
+template <class C>
+struct Loader {
+    const uint8_t *a[C::A_PW];
+    const uint8_t *b[C::B_PW];
+    const uint8_t *sb[C::SB_PW];
+    const uint8_t *sa[C::SA_PW];
+    bool has_sa;
+};
+
+template <class C>
+__device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, uint32_t s,
+                                           uint32_t wave) {
+#pragma unroll
+    for (int q = 0; q < C::A_PW; q++)
+        dma<16>(L.a[q] + 128u * s, stage + C::OFF_A + 1024 * (q * 4 + (int)wave));
+#pragma unroll
+    for (int q = 0; q < C::B_PW; q++)
+        dma<16>(L.b[q] + 64u * s, stage + C::OFF_B + 1024 * (q * 4 + (int)wave));
+#pragma unroll
+    for (int q = 0; q < C::SB_PW; q++)
+        dma<4>(L.sb[q] + 4u * s, stage + C::OFF_SB + 256 * (q * 4 + (int)wave));
+    if (L.has_sa) {
+#pragma unroll
+        for (int q = 0; q < C::SA_PW; q++)
+            dma<4>(L.sa[q] + 4u * s, stage + C::OFF_SA + 256 * (q * 4 + (int)wave));
+    }
+}
+
+/* Wait until this wave's loads of the step `ahead` steps back have landed:
+ * `ahead` later steps may stay in flight. */
+template <class C>
+__device__ __forceinline__ void wait_step(const Loader<C> &L, int ahead) {
+    if (ahead > 0) {
+        if (L.has_sa) wait_vm<C::LOADS_FULL>();
+        else wait_vm<C::LOADS_NO_SA>();
+    } else {
+        wait_vm<0>();
+    }
+}
+
+template <int... Is, class Fn>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, Fn &&f) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class Fn>
+__device__ __forceinline__ void static_for(Fn &&f) {
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
 }
 
 /*
- * acc[i][j] += A_i . W_j^T over K for this wave: A_i = activation rows of
- * m-subtile i (TERMS MXFP8 terms), W_j = weight rows of n-subtile j.
- * a_row[t][i] / a_scl[t][i] point at the lane's activation row (codes,
- * scales); w_row[j] / w_scl[j] at the lane's weight row.
+ * LDS reads of staged fragments are issued as inline asm: the compiler's
+ * wait insertion cannot tell which ring buffer an in-flight direct-to-LDS
+ * load targets and would drain them all before every read. The reads are
+ * completed by one explicit lgkmcnt(0) wait (mfma_step) and the results are
+ * passed through empty volatile asm after it, so no use can move above it.
  */
-template <int WM, int TERMS>
-__device__ __forceinline__ void mfma_rows(f32x4 (&acc)[WM][4], const uint8_t *(&a_row)[TERMS][WM],
-                                          const uint8_t *(&a_scl)[TERMS][WM],
-                                          const uint8_t *(&w_row)[4], const uint8_t *(&w_scl)[4],
-                                          uint32_t K, uint32_t g) {
-    for (uint32_t k0 = 0; k0 < K; k0 += 128u) {
-        const uint32_t kb = k0 / 32u + g;
-        i32x8 wf[4];
-        int ws[4];
+template <int OFF>
+__device__ __forceinline__ u32x4_t ds_read16(uint32_t addr) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t ds_read4(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+template <class T>
+__device__ __forceinline__ void after_wait(T &v) {
+    asm volatile("" : "+v"(v));
+}
+
+/* One K step from a staged LDS buffer: fragments, then the MFMAs. */
+template <class C>
+__device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
+                                          uint32_t wm, uint32_t wn) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t g = lane >> 4, c = lane & 15u;
+    const uint32_t base = lds_addr(st);
+    const uint32_t a_base = base + 16u * lane + 2048u * C::WM * wm;
+    const uint32_t b_base = base + 16u * lane + 1024u * C::WN * wn;
+    const uint32_t sa_base = base + 4u * c + 64u * C::WM * wm;
+    const uint32_t sb_base = base + 4u * c + 64u * C::WN * wn;
+    u32x4_t alo[C::TERMS][C::WM], ahi[C::TERMS][C::WM], bv[C::WN];
+    uint32_t saw[C::TERMS][C::WM], sbw[C::WN];
+    static_for<C::TERMS * C::WM>([&](auto I) {
+        constexpr int t = decltype(I)::value / C::WM, i = decltype(I)::value % C::WM;
+        constexpr int off = C::OFF_A + 2048 * (t * (C::BM / 16) + i);
+        alo[t][i] = ds_read16<off>(a_base);
+        ahi[t][i] = ds_read16<off + 1024>(a_base);
+        saw[t][i] = ds_read4<C::OFF_SA + 4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
+    });
+    static_for<C::WN>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        bv[j] = ds_read16<C::OFF_B + 1024 * j>(b_base);
+        sbw[j] = ds_read4<C::OFF_SB + 64 * j>(sb_base);
+    });
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            wf[j] = load_fp4_frag(w_row[j], k0, g);
-            ws[j] = (int)gload(w_scl[j] + kb);
+    for (int t = 0; t < C::TERMS; t++)
+#pragma unroll
+        for (int i = 0; i < C::WM; i++) {
+            after_wait(alo[t][i]);
+            after_wait(ahi[t][i]);
+            after_wait(saw[t][i]);
         }
-        i32x8 af[TERMS][WM];
-        int as[TERMS][WM];
 #pragma unroll
-        for (int t = 0; t < TERMS; t++)
+    for (int j = 0; j < C::WN; j++) {
+        after_wait(bv[j]);
+        after_wait(sbw[j]);
+    }
+    i32x8 af[C::TERMS][C::WM];
+    int sa[C::TERMS][C::WM];
 #pragma unroll
-            for (int i = 0; i < WM; i++) {
-                af[t][i] = load_fp8_frag(a_row[t][i], k0, g);
-                as[t][i] = (int)gload(a_scl[t][i] + kb);
-            }
+    for (int t = 0; t < C::TERMS; t++)
 #pragma unroll
-        for (int t = 0; t < TERMS; t++)
+        for (int i = 0; i < C::WM; i++) {
+            af[t][i] = i32x8{(int)alo[t][i].x, (int)alo[t][i].y, (int)alo[t][i].z,
+                             (int)alo[t][i].w, (int)ahi[t][i].x, (int)ahi[t][i].y,
+                             (int)ahi[t][i].z, (int)ahi[t][i].w};
+            sa[t][i] = (int)((saw[t][i] >> (8u * g)) & 255u);
+        }
+    i32x8 bf[C::WN];
+    int sb[C::WN];
 #pragma unroll
-            for (int i = 0; i < WM; i++)
+    for (int j = 0; j < C::WN; j++) {
+        bf[j] = i32x8{(int)bv[j].x, (int)bv[j].y, (int)bv[j].z, (int)bv[j].w, 0, 0, 0, 0};
+        sb[j] = (int)((sbw[j] >> (8u * g)) & 255u);
+    }
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        af[t][i], wf[j], acc[i][j], 0, 4, 0, as[t][i], 0, ws[j]);
+    for (int t = 0; t < C::TERMS; t++)
+#pragma unroll
+        for (int i = 0; i < C::WM; i++)
+#pragma unroll
+            for (int j = 0; j < C::WN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    af[t][i], bf[j], acc[i][j], 0, 4, 0, sa[t][i], 0, sb[j]);
+}
+
+/* Step s of the ring: wait for this wave's loads of step s (one later step
+ * may stay in flight), barrier (every wave's loads of s have landed and
+ * every wave is done reading the buffer refilled next), refill `nxt` with
+ * step s + 2, compute from `cur`. */
+template <class C>
+__device__ __forceinline__ void ring_step(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
+                                          const uint8_t *cur, uint8_t *nxt, uint32_t s,
+                                          uint32_t nsteps, uint32_t wm, uint32_t wn) {
+    wait_step<C>(L, s + 1u < nsteps ? 1 : 0);
+    __builtin_amdgcn_s_barrier();
+    if (s + 2u < nsteps) issue_step<C>(L, nxt, s + 2u, threadIdx.x >> 6);
+    mfma_step<C>(acc, cur, wm, wn);
+}
+
+/*
+ * acc[i][j] += A(wave rows i) . W(wave rows j)^T over K (K % 128 == 0)
+ * through three LDS buffers. They are distinct __shared__ arrays and the
+ * loop is unrolled by three so every access names its buffer statically:
+ * the compiler then sees that the in-flight direct-to-LDS loads target
+ * other buffers than the ones being read and does not drain them.
+ */
+template <class C>
+__device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
+                                              uint8_t *b0, uint8_t *b1, uint8_t *b2, uint32_t K,
+                                              uint32_t wm, uint32_t wn) {
+    static_assert(C::STAGES == 3, "three buffers");
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t nsteps = K / 128u;
+    issue_step<C>(L, b0, 0u, wave);
+    if (nsteps > 1u) issue_step<C>(L, b1, 1u, wave);
+    for (uint32_t s = 0; s < nsteps; s += 3u) {
+        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn);
+        if (s + 1u < nsteps) ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn);
+        if (s + 2u < nsteps) ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn);
     }
 }
 
@@ -204,76 +386,116 @@ struct GateUpArgs {
     float beta, lb;
 };
 
-/* grid (F / 128, tile cap), block 256. Wave w: gate and up rows
- * f0 + 32 w .. + 32 (n-subtiles 0, 1 = gate, 2, 3 = up). */
-template <int WM, int TERMS>
+/*
+ * grid (F / (BN / 2), tile cap), block 256, LDS C::LDS bytes. The block's
+ * BN weight rows are BN / 2 gate rows and the same up rows: wave column wn
+ * owns f-columns f0 + 8 WN wn .. + 8 WN, n-subtiles j < WN / 2 gate and
+ * j >= WN / 2 up, so gate and up of a column meet in one lane. Epilogue:
+ * activation, then the MXFP8 split of each 32-column block (two gate
+ * subtiles x 16 lanes).
+ */
+template <class C>
 __global__ __launch_bounds__(256) void gateup_mfma_kernel(GateUpArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
     const uint32_t tile = blockIdx.y;
     if (tile >= *A.tile_count) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15u;
+    const uint32_t wm = wave / C::NW, wn = wave % C::NW;
     const uint32_t e = A.tiles[3u * tile], row0 = A.tiles[3u * tile + 1u];
     const uint32_t rows = A.tiles[3u * tile + 2u];
     const uint32_t H = A.H, F = A.F;
     const k3_moe_expert ex = A.experts[e];
-    const uint32_t f0 = blockIdx.x * 128u + 32u * wave;
-
-    const uint8_t *w_row[4], *w_scl[4];
+    constexpr int FW = 8 * C::WN; /* f-columns per wave column */
+    const uint32_t f0 = blockIdx.x * (uint32_t)(C::BN / 2);
+    /* weight row of block subtile J, lane row c: gate rows for the first
+     * half of each wave column's subtiles, up rows (offset by F) after */
+    auto wrow = [&](int J, uint32_t cc) -> uint32_t {
+        const int wcol = J / C::WN, j = J % C::WN;
+        const uint32_t f = f0 + (uint32_t)(FW * wcol) + 16u * (uint32_t)(j % (C::WN / 2)) + cc;
+        return j < C::WN / 2 ? f : F + f; /* rows >= F address the up tensor */
+    };
+    auto tok = [&](uint32_t r) -> uint32_t {
+        return A.token_index[row0 + (r < rows ? r : 0u)];
+    };
+    auto a_row = [&](int t, uint32_t r) -> const uint8_t * {
+        return A.B.xq[t] + (uint64_t)tok(r) * H;
+    };
+    auto a_scl = [&](int t, uint32_t r) -> const uint8_t * {
+        return A.B.xs[t] + (uint64_t)tok(r) * (H / 32u);
+    };
+    Loader<C> L;
+    {
+        const uint8_t *gp = (const uint8_t *)ex.gate_packed, *up = (const uint8_t *)ex.up_packed;
+        const uint8_t *gs = (const uint8_t *)ex.gate_scales, *us = (const uint8_t *)ex.up_scales;
+        auto wr_codes = [&](int J, uint32_t cc) -> const uint8_t * {
+            const uint32_t r = wrow(J, cc);
+            return r < F ? gp + (uint64_t)r * (H / 2u) : up + (uint64_t)(r - F) * (H / 2u);
+        };
+        auto wr_scl = [&](int J, uint32_t cc) -> const uint8_t * {
+            const uint32_t r = wrow(J, cc);
+            return r < F ? gs + (uint64_t)r * (H / 32u) : us + (uint64_t)(r - F) * (H / 32u);
+        };
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t f = f0 + 16u * (uint32_t)(j & 1) + c;
-        const uint8_t *p = (const uint8_t *)(j < 2 ? ex.gate_packed : ex.up_packed);
-        const uint8_t *s = (const uint8_t *)(j < 2 ? ex.gate_scales : ex.up_scales);
-        w_row[j] = p + (uint64_t)f * (H / 2u);
-        w_scl[j] = s + (uint64_t)f * (H / 32u);
-    }
-    const uint8_t *a_row[TERMS][WM], *a_scl[TERMS][WM];
+        for (int q = 0; q < C::A_PW; q++) {
+            const int ch = q * 4 + (int)wave;
+            const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
+            L.a[q] = a_row(t, 16u * i + c) + 64u * h + 16u * g;
+        }
 #pragma unroll
-    for (int i = 0; i < WM; i++) {
-        const uint32_t r = 16u * i + c;
-        const uint32_t tok = A.token_index[row0 + (r < rows ? r : 0u)];
+        for (int q = 0; q < C::B_PW; q++) L.b[q] = wr_codes(q * 4 + (int)wave, c) + 16u * g;
 #pragma unroll
-        for (int t = 0; t < TERMS; t++) {
-            a_row[t][i] = A.B.xq[t] + (uint64_t)tok * H;
-            a_scl[t][i] = A.B.xs[t] + (uint64_t)tok * (H / 32u);
+        for (int q = 0; q < C::SB_PW; q++) L.sb[q] = wr_scl((q * 4 + (int)wave) * 4 + (int)g, c);
+        L.has_sa = C::SA_CH >= 4 || (int)wave < C::SA_CH;
+#pragma unroll
+        for (int q = 0; q < C::SA_PW; q++) {
+            const int ch = C::SA_CH >= 4 ? q * 4 + (int)wave : (int)wave % C::SA_CH;
+            const int t = ch / (C::SA_ROWS / 64);
+            const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
+            L.sa[q] = a_scl(t, r);
         }
     }
-    f32x4 acc[WM][4];
+    f32x4 acc[C::WM][C::WN];
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+    for (int i = 0; i < C::WM; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_rows<WM, TERMS>(acc, a_row, a_scl, w_row, w_scl, H, g);
+        for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    mfma_pipeline<C>(acc, L, b0, b1, b2, H, wm, wn);
 
-    /* epilogue: activation, then the MXFP8 split of each row's 32-column
-     * block (columns f0 .. f0 + 31 live in the 16 lanes of this g, two
-     * subtiles each) */
+    const uint32_t fw0 = f0 + (uint32_t)FW * wn;
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+    for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t lr = 16u * i + 4u * g + (uint32_t)r;
-            float v[2];
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                v[j] = bf16r(gated_act(bf16r(acc[i][j][r]), bf16r(acc[i][j + 2][r]), A.kind,
-                                       A.beta, A.lb));
+            const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
             const uint64_t prow = (uint64_t)row0 + (lr < rows ? lr : 0u);
 #pragma unroll
-            for (int t = 0; t < TERMS; t++) {
-                float amax = fmaxf(fabsf(v[0]), fabsf(v[1]));
+            for (int q = 0; q < C::WN / 4; q++) { /* 32-column blocks */
+                float v[2];
 #pragma unroll
-                for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-                const uint32_t sb = mx8_scale_byte(amax);
-                const float inv = mx8_inv_scale(sb), sc = e8m0_to_f32(sb);
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const uint32_t code = f32_to_e4m3(__fmul_rn(v[j], inv));
-                    if (lr < rows) A.B.aq[t][prow * F + f0 + 16u * j + c] = (uint8_t)code;
-                    if (TERMS == 2 && t == 0)
-                        v[j] = __fsub_rn(v[j], __fmul_rn(e4m3_to_f32(code), sc));
+                for (int h = 0; h < 2; h++) {
+                    const int jg = 2 * q + h;
+                    v[h] = bf16r(gated_act(bf16r(acc[i][jg][r]), bf16r(acc[i][C::WN / 2 + jg][r]),
+                                           A.kind, A.beta, A.lb));
                 }
-                if (lr < rows && c == 0u) A.B.as[t][prow * (F / 32u) + f0 / 32u] = (uint8_t)sb;
+#pragma unroll
+                for (int t = 0; t < C::TERMS; t++) {
+                    float amax = fmaxf(fabsf(v[0]), fabsf(v[1]));
+#pragma unroll
+                    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+                    const uint32_t sbyte = mx8_scale_byte(amax);
+                    const float inv = mx8_inv_scale(sbyte), sc = e8m0_to_f32(sbyte);
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t code = f32_to_e4m3(__fmul_rn(v[h], inv));
+                        if (lr < rows)
+                            A.B.aq[t][prow * F + fw0 + 32u * q + 16u * h + c] = (uint8_t)code;
+                        if (C::TERMS == 2 && t == 0)
+                            v[h] = __fsub_rn(v[h], __fmul_rn(e4m3_to_f32(code), sc));
+                    }
+                    if (lr < rows && c == 0u)
+                        A.B.as[t][prow * (F / 32u) + fw0 / 32u + q] = (uint8_t)sbyte;
+                }
             }
         }
 }
@@ -292,54 +514,82 @@ struct DownArgs {
     uint32_t H, F;
 };
 
-/* grid (H / 256, tile cap), block 256. Wave w: down rows d0 + 64 w .. + 64. */
-template <int WM, int TERMS>
+/* grid (H / BN, tile cap), block 256: y[route] rows d0 .. d0 + BN. */
+template <class C>
 __global__ __launch_bounds__(256) void down_mfma_kernel(DownArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
     const uint32_t tile = blockIdx.y;
     if (tile >= *A.tile_count) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15u;
+    const uint32_t wm = wave / C::NW, wn = wave % C::NW;
     const uint32_t e = A.tiles[3u * tile], row0 = A.tiles[3u * tile + 1u];
     const uint32_t rows = A.tiles[3u * tile + 2u];
     const uint32_t H = A.H, F = A.F;
     const k3_moe_expert ex = A.experts[e];
-    const uint32_t d0 = blockIdx.x * 256u + 64u * wave;
-
-    const uint8_t *w_row[4], *w_scl[4];
+    const uint32_t d0 = blockIdx.x * (uint32_t)C::BN;
+    const uint8_t *wp = (const uint8_t *)ex.down_packed, *ws = (const uint8_t *)ex.down_scales;
+    auto prow = [&](uint32_t r) -> uint64_t { return (uint64_t)row0 + (r < rows ? r : 0u); };
+    Loader<C> L;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t d = d0 + 16u * j + c;
-        w_row[j] = (const uint8_t *)ex.down_packed + (uint64_t)d * (F / 2u);
-        w_scl[j] = (const uint8_t *)ex.down_scales + (uint64_t)d * (F / 32u);
+    for (int q = 0; q < C::A_PW; q++) {
+        const int ch = q * 4 + (int)wave;
+        const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
+        L.a[q] = A.B.aq[t] + prow(16u * i + c) * F + 64u * h + 16u * g;
     }
-    const uint8_t *a_row[TERMS][WM], *a_scl[TERMS][WM];
 #pragma unroll
-    for (int i = 0; i < WM; i++) {
-        const uint32_t r = 16u * i + c;
-        const uint64_t prow = (uint64_t)row0 + (r < rows ? r : 0u);
+    for (int q = 0; q < C::B_PW; q++)
+        L.b[q] = wp + (uint64_t)(d0 + 16u * (q * 4 + wave) + c) * (F / 2u) + 16u * g;
 #pragma unroll
-        for (int t = 0; t < TERMS; t++) {
-            a_row[t][i] = A.B.aq[t] + prow * F;
-            a_scl[t][i] = A.B.as[t] + prow * (F / 32u);
-        }
+    for (int q = 0; q < C::SB_PW; q++)
+        L.sb[q] = ws + (uint64_t)(d0 + 64u * (q * 4 + wave) + lane) * (F / 32u);
+    L.has_sa = C::SA_CH >= 4 || (int)wave < C::SA_CH;
+#pragma unroll
+    for (int q = 0; q < C::SA_PW; q++) {
+        const int ch = C::SA_CH >= 4 ? q * 4 + (int)wave : (int)wave % C::SA_CH;
+        const int t = ch / (C::SA_ROWS / 64);
+        const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
+        L.sa[q] = A.B.as[t] + prow(r) * (F / 32u);
     }
-    f32x4 acc[WM][4];
+    f32x4 acc[C::WM][C::WN];
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+    for (int i = 0; i < C::WM; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_rows<WM, TERMS>(acc, a_row, a_scl, w_row, w_scl, F, g);
+        for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    mfma_pipeline<C>(acc, L, b0, b1, b2, F, wm, wn);
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+    for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t lr = 16u * i + 4u * g + (uint32_t)r;
+            const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
             if (lr >= rows) continue;
             const uint64_t route = A.route_index[row0 + lr];
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                A.y[route * H + d0 + 16u * j + c] = f32_to_bf16(acc[i][j][r]);
+            for (int j = 0; j < C::WN; j++)
+                A.y[route * H + d0 + 16u * (wn * C::WN + (uint32_t)j) + c] =
+                    f32_to_bf16(acc[i][j][r]);
         }
+}
+
+/* Tile classes (rows per tile): 16, 64, 128. One-term class 0 computes
+ * 32 rows so that its A chunks still split over four waves. */
+template <int TERMS>
+using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3>;
+template <int TERMS>
+using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 3>;
+template <int TERMS>
+using Cls2 = TileCfg<2, 2, 4, 8, TERMS, 3>;
+
+template <class C>
+void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C>), dim3(a.F / (C::BN / 2), cap),
+                       dim3(256), 0, st, a);
+}
+
+template <class C>
+void launch_down(const DownArgs &a, uint32_t cap, hipStream_t st) {
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(a.H / C::BN, cap), dim3(256), 0,
+                       st, a);
 }
 
 template <int TERMS>
@@ -367,20 +617,18 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         if (!B.tile_cap[c]) continue;
         ga.tiles = tl[c];
         ga.tile_count = B.tile_count + c;
-        const dim3 grid(F / 128u, B.tile_cap[c]);
-        if (c == 0) hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<1, TERMS>), grid, dim3(256), 0, st, ga);
-        if (c == 1) hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<2, TERMS>), grid, dim3(256), 0, st, ga);
-        if (c == 2) hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<4, TERMS>), grid, dim3(256), 0, st, ga);
+        if (c == 0) launch_gateup<Cls0<TERMS>>(ga, B.tile_cap[c], st);
+        if (c == 1) launch_gateup<Cls1<TERMS>>(ga, B.tile_cap[c], st);
+        if (c == 2) launch_gateup<Cls2<TERMS>>(ga, B.tile_cap[c], st);
     }
     mark(K3_MOE_STAGE_DOWN);
     for (int c = 0; c < 3; c++) {
         if (!B.tile_cap[c]) continue;
         da.tiles = tl[c];
         da.tile_count = B.tile_count + c;
-        const dim3 grid(H / 256u, B.tile_cap[c]);
-        if (c == 0) hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<1, TERMS>), grid, dim3(256), 0, st, da);
-        if (c == 1) hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<2, TERMS>), grid, dim3(256), 0, st, da);
-        if (c == 2) hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<4, TERMS>), grid, dim3(256), 0, st, da);
+        if (c == 0) launch_down<Cls0<TERMS>>(da, B.tile_cap[c], st);
+        if (c == 1) launch_down<Cls1<TERMS>>(da, B.tile_cap[c], st);
+        if (c == 2) launch_down<Cls2<TERMS>>(da, B.tile_cap[c], st);
     }
     return hipGetLastError() == hipSuccess;
 }
@@ -391,7 +639,7 @@ void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[3]) {
     const uint64_t R = (uint64_t)T * k;
     caps[0] = (uint32_t)(R < E ? R : E);
     caps[1] = (uint32_t)(R / 17u < E ? R / 17u : E);
-    caps[2] = (uint32_t)(R / 64u + (R / 33u < E ? R / 33u : E));
+    caps[2] = (uint32_t)(R / 128u + (R / 65u < E ? R / 65u : E));
 }
 
 bool mfma_supported(const k3_moe_shape &s) {
