@@ -13,9 +13,9 @@
  *                   the activation. 4096 blocks keep ~64 MB of loads in
  *                   flight.
  *   down_kernel     one block per 8 output rows for all k slots (each wave
- *                   streams contiguous 8-row stripes of four slots'
- *                   down matrices, double-buffered), then the rank-order
- *                   weighted combine plus the residual.
+ *                   streams contiguous 8-row stripes of four slots' down
+ *                   matrices), then the rank-order weighted combine plus
+ *                   the residual.
  *
  * Every hand-off is a kernel boundary, so all loads and stores are plain
  * (cached). Fusing the stages into one launch was measured and dropped on
@@ -197,56 +197,40 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
 /*
  * grid (H / kRB), block 256: the block computes output rows rb*kRB..+kRB
  * (a contiguous kRB-row stripe of each selected down matrix) for all k
- * slots -- wave w handles slots w, w + 4, ..., with the next slot's loads
- * in flight while the current one is reduced; lane l owns groups l, l + 64,
+ * slots -- wave w handles slots w, w + 4, ... one at a time, so the block
+ * reads four kRB-row runs at once; lane l owns groups l, l + 64,
  * ... (M of them: F <= 2048 * M) -- then combines the k bf16 slot outputs
  * in rank order with the residual: out[d] = bf16(residual[d] +
  * bf16(sum_r w[r] * y[r, d])), product and sum rounded separately
  * (k3_rocm_ops.cu:1452-1510).
  */
 template <int M>
-struct DownTile {
-    uint4 w[kRB][M];
-    uint32_t sc[kRB][M];
-};
-
-template <int M>
-__device__ __forceinline__ bool down_issue(const DecodeParams &P, uint32_t slot, uint32_t row0,
-                                           DownTile<M> &t) {
-    if (slot >= P.top_k) return false;
-    const k3_moe_expert ex = P.sel[slot];
-    if (!ex.down_packed) return false;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t F = P.ffn, G = F / 32u;
-    const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
-    const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
-#pragma unroll
-    for (int i = 0; i < kRB; i++)
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            const uint32_t g = lane + 64u * m;
-            if (g < G) {
-                t.w[i][m] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g));
-                t.sc[i][m] = gload(ds + (uint64_t)i * G + g);
-            }
-        }
-    return true;
-}
-
-template <int M>
 __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
     __shared__ float ys[32][kRB];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t waves = blockDim.x >> 6;
     const uint32_t row0 = blockIdx.x * kRB;
     const uint32_t F = P.ffn, G = F / 32u;
-    DownTile<M> cur, nxt;
-    bool on = down_issue<M>(P, wave, row0, cur);
-    for (uint32_t slot = wave; slot < P.top_k; slot += 4u) {
-        const bool on_next = down_issue<M>(P, slot + 4u, row0, nxt);
+    for (uint32_t slot = wave; slot < P.top_k; slot += waves) {
         float acc[kRB];
 #pragma unroll
         for (int i = 0; i < kRB; i++) acc[i] = 0.0f;
-        if (on) {
+        const k3_moe_expert ex = P.sel[slot];
+        if (ex.down_packed) {
+            const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
+            const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
+            uint4 w[kRB][M];
+            uint32_t sc[kRB][M];
+#pragma unroll
+            for (int i = 0; i < kRB; i++)
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const uint32_t g = lane + 64u * m;
+                    if (g < G) {
+                        w[i][m] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g));
+                        sc[i][m] = gload(ds + (uint64_t)i * G + g);
+                    }
+                }
             const uint4 *a4 = (const uint4 *)(P.act + (uint64_t)slot * F);
 #pragma unroll
             for (int m = 0; m < M; m++) {
@@ -256,16 +240,13 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
                     bf16x32_to_f32(a4 + 4u * g, xf);
 #pragma unroll
                     for (int i = 0; i < kRB; i++)
-                        acc[i] = fmaf(fp4_group(cur.w[i][m], xf), e8m0_to_f32(cur.sc[i][m]),
-                                      acc[i]);
+                        acc[i] = fmaf(fp4_group(w[i][m], xf), e8m0_to_f32(sc[i][m]), acc[i]);
                 }
             }
         }
         const float v = wave_sum_rows<kRB>(acc);
         const int owner = wave_rows_owner<kRB>();
         if ((lane & (64u / kRB - 1u)) == 0u) ys[slot][owner] = bf16_to_f32(f32_to_bf16(v));
-        cur = nxt;
-        on = on_next;
     }
     __syncthreads();
     if (threadIdx.x < (uint32_t)kRB) {
@@ -302,10 +283,11 @@ bool decode_launch_experts(const DecodeParams &P, hipStream_t st, const StageMar
     mark(K3_MOE_STAGE_GATE_UP);
     hipLaunchKernelGGL(gateup_kernel, dim3(P.ffn / kGU, P.top_k), dim3(256), 0, st, P);
     mark(K3_MOE_STAGE_DOWN);
+    const dim3 block(256);
     if (P.ffn <= 2048u)
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(down_kernel<1>), dim3(P.hidden / kRB), dim3(256), 0, st, P);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(down_kernel<1>), dim3(P.hidden / kRB), block, 0, st, P);
     else
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(down_kernel<2>), dim3(P.hidden / kRB), dim3(256), 0, st, P);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(down_kernel<2>), dim3(P.hidden / kRB), block, 0, st, P);
     mark(K3_MOE_STAGE_COMBINE); /* folded into down */
     mark(K3_MOE_STAGE_END);
     return hipGetLastError() == hipSuccess;

@@ -152,10 +152,20 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
  * waves in equal numbers per kind; the A scale chunks of small tiles (fewer
  * than four) go to the first waves.
  */
+/* How the chunks of one kind are dealt to the block's W waves: N >= W
+ * chunks must split evenly (wave w takes w, w + W, ...); fewer go one each
+ * to the first N waves. */
+template <int N, int W>
+struct Deal {
+    static constexpr bool partial = N < W;
+    static constexpr int per = N == 0 ? 0 : (partial ? 1 : N / W);
+    static_assert(partial || N % W == 0, "chunks split evenly over the waves");
+};
+
 template <int MW_, int NW_, int WM_, int WN_, int TERMS_, int STAGES_>
 struct TileCfg {
     static constexpr int MW = MW_, NW = NW_, WM = WM_, WN = WN_, TERMS = TERMS_;
-    static constexpr int STAGES = STAGES_;
+    static constexpr int STAGES = STAGES_, NWV = MW * NW, THREADS = 64 * NWV;
     static constexpr int BM = MW * 16 * WM, BN = NW * 16 * WN;
     static constexpr int A_CH = TERMS * (BM / 16) * 2, B_CH = BN / 16;
     static constexpr int SA_ROWS = BM < 64 ? 64 : BM;
@@ -163,14 +173,18 @@ struct TileCfg {
     static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, OFF_SA = OFF_B + B_CH * 1024;
     static constexpr int OFF_SB = OFF_SA + SA_CH * 256, STAGE = OFF_SB + SB_CH * 256;
     static constexpr int LDS = STAGE * STAGES;
-    static constexpr int A_PW = A_CH / 4, B_PW = B_CH / 4, SB_PW = SB_CH / 4;
-    static constexpr int SA_PW = SA_CH >= 4 ? SA_CH / 4 : 1; /* waves < SA_CH when SA_CH < 4 */
-    static constexpr int LOADS_FULL = A_PW + B_PW + SB_PW + SA_PW;
-    static constexpr int LOADS_NO_SA = A_PW + B_PW + SB_PW + (SA_CH >= 4 ? SA_PW : 0);
-    static_assert(MW * NW == 4, "four waves");
-    static_assert(A_CH % 4 == 0 && B_CH % 4 == 0 && SB_CH % 4 == 0, "chunks split evenly");
-    static_assert(SA_CH >= 4 ? SA_CH % 4 == 0 : true, "scale chunks");
+    using DA = Deal<A_CH, NWV>;
+    using DB = Deal<B_CH, NWV>;
+    using DSA = Deal<SA_CH, NWV>;
+    using DSB = Deal<SB_CH, NWV>;
+    /* loads per step of a wave holding the kinds flagged in `mask`
+     * (bit 3 A, 2 B, 1 SA, 0 SB) */
+    static constexpr int loads(int mask) {
+        return ((mask & 8) ? DA::per : 0) + ((mask & 4) ? DB::per : 0) +
+               ((mask & 2) ? DSA::per : 0) + ((mask & 1) ? DSB::per : 0);
+    }
     static_assert(LDS <= 160 * 1024, "LDS");
+    static_assert(loads(15) < 32, "vmcnt budget for one step in flight");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -190,46 +204,60 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-/* Per-lane source pointers of the chunks this wave loads. */
+/* Per-lane source pointers of the chunks this wave loads, and which kinds
+ * it holds (index q of a kind is chunk q * NWV + wave, or chunk `wave`). */
 template <class C>
 struct Loader {
-    const uint8_t *a[C::A_PW];
-    const uint8_t *b[C::B_PW];
-    const uint8_t *sb[C::SB_PW];
-    const uint8_t *sa[C::SA_PW];
-    bool has_sa;
+    const uint8_t *a[C::DA::per > 0 ? C::DA::per : 1];
+    const uint8_t *b[C::DB::per > 0 ? C::DB::per : 1];
+    const uint8_t *sa[C::DSA::per > 0 ? C::DSA::per : 1];
+    const uint8_t *sb[C::DSB::per > 0 ? C::DSB::per : 1];
+    uint32_t mask; /* kinds held: bit 3 A, 2 B, 1 SA, 0 SB */
 };
+
+/* chunk index of slot q of a kind for this wave */
+template <class D, int W>
+__device__ __forceinline__ int chunk_of(int q, uint32_t wave) {
+    return D::partial ? (int)wave : q * W + (int)wave;
+}
+
+template <class C>
+__device__ __forceinline__ uint32_t kinds_held(uint32_t wave) {
+    auto has = [&](bool partial, int n) { return !partial || (int)wave < n; };
+    return (has(C::DA::partial, C::A_CH) ? 8u : 0u) | (has(C::DB::partial, C::B_CH) ? 4u : 0u) |
+           (has(C::DSA::partial, C::SA_CH) ? 2u : 0u) | (has(C::DSB::partial, C::SB_CH) ? 1u : 0u);
+}
 
 template <class C>
 __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, uint32_t s,
                                            uint32_t wave) {
+    constexpr int W = C::NWV;
+    if (L.mask & 8u) {
 #pragma unroll
-    for (int q = 0; q < C::A_PW; q++)
-        dma<16>(L.a[q] + 128u * s, stage + C::OFF_A + 1024 * (q * 4 + (int)wave));
+        for (int q = 0; q < C::DA::per; q++)
+            dma<16>(L.a[q] + 128u * s, stage + C::OFF_A + 1024 * chunk_of<typename C::DA, W>(q, wave));
+    }
+    if (L.mask & 4u) {
 #pragma unroll
-    for (int q = 0; q < C::B_PW; q++)
-        dma<16>(L.b[q] + 64u * s, stage + C::OFF_B + 1024 * (q * 4 + (int)wave));
+        for (int q = 0; q < C::DB::per; q++)
+            dma<16>(L.b[q] + 64u * s, stage + C::OFF_B + 1024 * chunk_of<typename C::DB, W>(q, wave));
+    }
+    if (L.mask & 2u) {
 #pragma unroll
-    for (int q = 0; q < C::SB_PW; q++)
-        dma<4>(L.sb[q] + 4u * s, stage + C::OFF_SB + 256 * (q * 4 + (int)wave));
-    if (L.has_sa) {
+        for (int q = 0; q < C::DSA::per; q++)
+            dma<4>(L.sa[q] + 4u * s, stage + C::OFF_SA + 256 * chunk_of<typename C::DSA, W>(q, wave));
+    }
+    if (L.mask & 1u) {
 #pragma unroll
-        for (int q = 0; q < C::SA_PW; q++)
-            dma<4>(L.sa[q] + 4u * s, stage + C::OFF_SA + 256 * (q * 4 + (int)wave));
+        for (int q = 0; q < C::DSB::per; q++)
+            dma<4>(L.sb[q] + 4u * s, stage + C::OFF_SB + 256 * chunk_of<typename C::DSB, W>(q, wave));
     }
 }
 
-/* Wait until this wave's loads of the step `ahead` steps back have landed:
- * `ahead` later steps may stay in flight. */
+/* Wait until this wave's loads of the current step have landed; with
+ * `ahead`, the following step's loads may stay in flight. */
 template <class C>
-__device__ __forceinline__ void wait_step(const Loader<C> &L, int ahead) {
-    if (ahead > 0) {
-        if (L.has_sa) wait_vm<C::LOADS_FULL>();
-        else wait_vm<C::LOADS_NO_SA>();
-    } else {
-        wait_vm<0>();
-    }
-}
+__device__ __forceinline__ void wait_step(const Loader<C> &L, int ahead);
 
 template <int... Is, class Fn>
 __device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...>, Fn &&f) {
@@ -238,6 +266,17 @@ __device__ __forceinline__ void static_for_impl(std::integer_sequence<int, Is...
 template <int N, class Fn>
 __device__ __forceinline__ void static_for(Fn &&f) {
     static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+template <class C>
+__device__ __forceinline__ void wait_step(const Loader<C> &L, int ahead) {
+    if (ahead <= 0) {
+        wait_vm<0>();
+        return;
+    }
+    static_for<16>([&](auto M) {
+        if (L.mask == (uint32_t)decltype(M)::value) wait_vm<C::loads(decltype(M)::value)>();
+    });
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -387,7 +426,7 @@ struct GateUpArgs {
 };
 
 /*
- * grid (F / (BN / 2), tile cap), block 256, LDS C::LDS bytes. The block's
+ * grid (F / (BN / 2), tile cap), block C::THREADS, LDS C::LDS bytes. The block's
  * BN weight rows are BN / 2 gate rows and the same up rows: wave column wn
  * owns f-columns f0 + 8 WN wn .. + 8 WN, n-subtiles j < WN / 2 gate and
  * j >= WN / 2 up, so gate and up of a column meet in one lane. Epilogue:
@@ -395,7 +434,7 @@ struct GateUpArgs {
  * subtiles x 16 lanes).
  */
 template <class C>
-__global__ __launch_bounds__(256) void gateup_mfma_kernel(GateUpArgs A) {
+__global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
     const uint32_t tile = blockIdx.y;
     if (tile >= *A.tile_count) return;
@@ -436,20 +475,27 @@ __global__ __launch_bounds__(256) void gateup_mfma_kernel(GateUpArgs A) {
             const uint32_t r = wrow(J, cc);
             return r < F ? gs + (uint64_t)r * (H / 32u) : us + (uint64_t)(r - F) * (H / 32u);
         };
+        constexpr int W = C::NWV;
+        L.mask = kinds_held<C>(wave);
 #pragma unroll
-        for (int q = 0; q < C::A_PW; q++) {
-            const int ch = q * 4 + (int)wave;
+        for (int q = 0; q < C::DA::per; q++) {
+            const int ch = min(chunk_of<typename C::DA, W>(q, wave), C::A_CH - 1);
             const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
             L.a[q] = a_row(t, 16u * i + c) + 64u * h + 16u * g;
         }
 #pragma unroll
-        for (int q = 0; q < C::B_PW; q++) L.b[q] = wr_codes(q * 4 + (int)wave, c) + 16u * g;
+        for (int q = 0; q < C::DB::per; q++) {
+            const int J = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
+            L.b[q] = wr_codes(J, c) + 16u * g;
+        }
 #pragma unroll
-        for (int q = 0; q < C::SB_PW; q++) L.sb[q] = wr_scl((q * 4 + (int)wave) * 4 + (int)g, c);
-        L.has_sa = C::SA_CH >= 4 || (int)wave < C::SA_CH;
+        for (int q = 0; q < C::DSB::per; q++) {
+            const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
+            L.sb[q] = wr_scl(ch * 4 + (int)g, c); /* 64 rows = 4 subtiles per chunk */
+        }
 #pragma unroll
-        for (int q = 0; q < C::SA_PW; q++) {
-            const int ch = C::SA_CH >= 4 ? q * 4 + (int)wave : (int)wave % C::SA_CH;
+        for (int q = 0; q < C::DSA::per; q++) {
+            const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
             const int t = ch / (C::SA_ROWS / 64);
             const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
             L.sa[q] = a_scl(t, r);
@@ -514,9 +560,9 @@ struct DownArgs {
     uint32_t H, F;
 };
 
-/* grid (H / BN, tile cap), block 256: y[route] rows d0 .. d0 + BN. */
+/* grid (H / BN, tile cap), block C::THREADS: y[route] rows d0 .. d0 + BN. */
 template <class C>
-__global__ __launch_bounds__(256) void down_mfma_kernel(DownArgs A) {
+__global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
     const uint32_t tile = blockIdx.y;
     if (tile >= *A.tile_count) return;
@@ -531,22 +577,27 @@ __global__ __launch_bounds__(256) void down_mfma_kernel(DownArgs A) {
     const uint8_t *wp = (const uint8_t *)ex.down_packed, *ws = (const uint8_t *)ex.down_scales;
     auto prow = [&](uint32_t r) -> uint64_t { return (uint64_t)row0 + (r < rows ? r : 0u); };
     Loader<C> L;
+    constexpr int W = C::NWV;
+    L.mask = kinds_held<C>(wave);
 #pragma unroll
-    for (int q = 0; q < C::A_PW; q++) {
-        const int ch = q * 4 + (int)wave;
+    for (int q = 0; q < C::DA::per; q++) {
+        const int ch = min(chunk_of<typename C::DA, W>(q, wave), C::A_CH - 1);
         const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
         L.a[q] = A.B.aq[t] + prow(16u * i + c) * F + 64u * h + 16u * g;
     }
 #pragma unroll
-    for (int q = 0; q < C::B_PW; q++)
-        L.b[q] = wp + (uint64_t)(d0 + 16u * (q * 4 + wave) + c) * (F / 2u) + 16u * g;
+    for (int q = 0; q < C::DB::per; q++) {
+        const int J = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
+        L.b[q] = wp + (uint64_t)(d0 + 16u * J + c) * (F / 2u) + 16u * g;
+    }
 #pragma unroll
-    for (int q = 0; q < C::SB_PW; q++)
-        L.sb[q] = ws + (uint64_t)(d0 + 64u * (q * 4 + wave) + lane) * (F / 32u);
-    L.has_sa = C::SA_CH >= 4 || (int)wave < C::SA_CH;
+    for (int q = 0; q < C::DSB::per; q++) {
+        const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
+        L.sb[q] = ws + (uint64_t)(d0 + 64u * ch + lane) * (F / 32u);
+    }
 #pragma unroll
-    for (int q = 0; q < C::SA_PW; q++) {
-        const int ch = C::SA_CH >= 4 ? q * 4 + (int)wave : (int)wave % C::SA_CH;
+    for (int q = 0; q < C::DSA::per; q++) {
+        const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
         const int t = ch / (C::SA_ROWS / 64);
         const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
         L.sa[q] = A.B.as[t] + prow(r) * (F / 32u);
@@ -578,18 +629,18 @@ using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3>;
 template <int TERMS>
 using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 3>;
 template <int TERMS>
-using Cls2 = TileCfg<2, 2, 4, 8, TERMS, 3>;
+using Cls2 = TileCfg<2, 4, 4, 4, TERMS, 3>; /* 8 waves: two per SIMD */
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
     hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C>), dim3(a.F / (C::BN / 2), cap),
-                       dim3(256), 0, st, a);
+                       dim3(C::THREADS), 0, st, a);
 }
 
 template <class C>
 void launch_down(const DownArgs &a, uint32_t cap, hipStream_t st) {
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(a.H / C::BN, cap), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(a.H / C::BN, cap),
+                       dim3(C::THREADS), 0, st, a);
 }
 
 template <int TERMS>
