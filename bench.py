@@ -69,6 +69,20 @@ def gate_up_bytes(cfg, T, unique):
     return unique * per + T * cfg.hidden * 2 + T * cfg.top_k * (4 + 2 * cfg.ffn)
 
 
+def recorded_traffic(workload, T, precision):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, each scaled by what
+    the same counter reads for a plain copy of known size), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(f"{workload}/T{T}/p{precision}")
+    except (OSError, ValueError):
+        return None
+    return rec["bytes"] if rec else None
+
+
 def cpu_baseline(cfg, inputs_cpu, store, budget_s, threads):
     sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
     import _oracle as O  # CPU checker / baseline only
@@ -107,7 +121,14 @@ def main():
     ap.add_argument("--tokens", type=int, default=0, help="override token count")
     ap.add_argument("--precision", type=int, default=0, help="0 exact, 1 mx8")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--rotate", type=int, default=0,
+                    help="distinct token batches cycled through the steps (default: 16 for "
+                         "T = 1, so consecutive steps route to different experts and no step "
+                         "finds its weights in the 256 MB last-level cache; 1 for T > 1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB, --steps times (the known-size "
+                         "kernel that scales FETCH_SIZE/WRITE_SIZE counter readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
@@ -115,6 +136,16 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": args.steps}), flush=True)
+        return
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from moonshine_amd import layer as L
@@ -124,11 +155,12 @@ def main():
     cfg = CONFIGS[args.config]
     T = args.tokens or cfg.tokens
     log(f"bench: {cfg.name} T={T} building resident expert store ...")
-    inputs = make_inputs(cfg, tokens=T)
+    R = args.rotate or (16 if T == 1 else 1)
+    inputs = make_inputs(cfg, tokens=T * R)
     moe = L.build_layer(cfg, inputs, device="cuda")
-    x = L.bf16_tensor(inputs.hidden)
-    r = L.bf16_tensor(inputs.residual)
-    out = torch.empty_like(x)
+    xs = L.bf16_tensor(inputs.hidden).view(R, T, cfg.hidden)
+    rs = L.bf16_tensor(inputs.residual).view(R, T, cfg.hidden)
+    out = torch.empty((T, cfg.hidden), dtype=xs.dtype, device=xs.device)
     ids = torch.zeros((T, cfg.top_k), dtype=torch.int32, device="cuda")
     wts = torch.zeros((T, cfg.top_k), dtype=torch.float32, device="cuda")
     ws = moe.workspace(T)
@@ -140,22 +172,28 @@ def main():
         for i in range(len(STAGES)):
             p.stage_events[i] = hip.event().value
     P = lambda t: ctypes.c_void_p(t.data_ptr())
-    argv = [P(out), P(x), P(r), P(moe.router_weight), P(moe.router_bias), P(moe.store.table),
-            ctypes.byref(moe.shape), T, args.precision, P(ids), P(wts), P(ws), ws.numel()]
+    argvs = [[P(out), P(xs[i]), P(rs[i]), P(moe.router_weight), P(moe.router_bias),
+              P(moe.store.table), ctypes.byref(moe.shape), T, args.precision, P(ids), P(wts),
+              P(ws), ws.numel()] for i in range(R)]
+    unique_per_batch = []
 
-    def step(profile):
-        if not lib().k3_moe_forward_profiled_bf16(*argv, profile, ctypes.c_void_p(stream)):
+    def step(i, profile):
+        if not lib().k3_moe_forward_profiled_bf16(*argvs[i % R], profile,
+                                                  ctypes.c_void_p(stream)):
             raise RuntimeError("k3_moe_forward_profiled_bf16 failed")
 
-    log(f"bench: warmup {args.warmup} ...")
-    for _ in range(args.warmup):
-        step(None)
+    log(f"bench: warmup {args.warmup} ({R} distinct token batches) ...")
+    for i in range(max(args.warmup, R)):
+        step(i, None)
+        if i < R:
+            torch.cuda.synchronize()
+            unique_per_batch.append(int(np.unique(ids.cpu().numpy()).size))
     torch.cuda.synchronize()
     log(f"bench: timing {args.steps} steps ...")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(None)
+        step(i, None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
@@ -164,7 +202,7 @@ def main():
     # apportions time; `value` comes from the event-free pass above)
     log(f"bench: {args.steps} profiled steps ...")
     for i in range(args.steps):
-        step(ctypes.byref(profiles[i]))
+        step(i, ctypes.byref(profiles[i]))
     torch.cuda.synchronize()
 
     stage_ms = {s: 0.0 for s in STAGES[:-1]}
@@ -175,14 +213,33 @@ def main():
             stage_ms[s] += hip.elapsed_ms(ev[i], ev[i + 1]) / args.steps
         gpu_ms += hip.elapsed_ms(ev[0], ev[-1]) / args.steps
 
-    ids_h = ids.cpu().numpy()
-    unique = int(np.unique(ids_h).size)
+    # steps cycle through the R batches: the mean over them is each step's work
+    unique = float(np.mean([unique_per_batch[i % R] for i in range(args.steps)]))
     total_bytes = algorithmic_bytes(cfg, T, unique)
     flops = T * cfg.top_k * 2 * 3 * cfg.ffn * cfg.hidden
-    kname = "gateup_kernel" if T == 1 else "grouped_gateup_kernel"
-    kbytes, kms = gate_up_bytes(cfg, T, unique), stage_ms["gate_up"]
-    achieved = kbytes / (kms * 1e-3) / 1e9
+    kms = stage_ms["gate_up"]
     layer_gbps = total_bytes / (ms_per_step * 1e-3) / 1e9
+    traffic = recorded_traffic(cfg.name, T, args.precision)
+    if T == 1:
+        kbytes = gate_up_bytes(cfg, T, unique)
+        achieved = kbytes / (kms * 1e-3) / 1e9
+        roofline = {"kernel": "gateup_kernel", "bound": "hbm", "achieved": achieved,
+                    "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                    "traffic": traffic, "algorithmic_bytes": kbytes, "avg_ms": kms}
+    else:
+        # grouped gate/up on scaled MFMA: useful MXFP4-product flops (gate and
+        # up, every route) over the stage time, against the dense MXFP4 peak
+        # named by the target; fp8_instr_frac prices the same time against
+        # the fp8 rate of the mixed fp8 x fp4 instruction actually issued
+        kflops = T * cfg.top_k * 2 * 2 * cfg.ffn * cfg.hidden
+        achieved = kflops / (kms * 1e-3) / 1e12
+        terms = 2 if args.precision == 1 else 1
+        roofline = {"kernel": "gateup_mfma_kernel", "bound": "mfma", "achieved": achieved,
+                    "peak": MXFP4_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": achieved / MXFP4_PEAK_TFLOPS, "traffic": traffic,
+                    "algorithmic_flops": kflops, "avg_ms": kms,
+                    "mfma_terms": terms,
+                    "fp8_instr_frac": achieved * terms / FP8_PEAK_TFLOPS}
     result = {
         "metric": "routed-MoE layer tok/s; decode HBM GB/s; 8K-prefill MXFP4 TFLOP/s",
         "value": T / (ms_per_step * 1e-3),
@@ -199,14 +256,12 @@ def main():
         "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden,
                    "experts": cfg.experts, "top_k": cfg.top_k, "ffn": cfg.ffn,
                    "activation": "swiglu" if cfg.activation == 1 else "situ",
-                   "scale": cfg.scale, "precision": ["exact", "mx8"][args.precision],
-                   "unique_experts": unique},
+                   "scale": cfg.scale, "precision": ["exact", "mx8", "mx8-1term"][args.precision],
+                   "unique_experts": unique, "distinct_batches": R},
         "layer": {"bytes": total_bytes, "hbm_gbps": layer_gbps,
                   "hbm_frac": layer_gbps / HBM_PEAK_GBPS, "tflops": flops / (ms_per_step * 1e-3) / 1e12,
                   "gpu_ms_events": gpu_ms, "stage_ms": stage_ms},
-        "roofline": {"kernel": kname, "bound": "hbm", "achieved": achieved,
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
-                     "traffic": None, "algorithmic_bytes": kbytes, "avg_ms": kms},
+        "roofline": roofline,
     }
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (C oracle) ...")

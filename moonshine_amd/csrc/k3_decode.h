@@ -24,6 +24,8 @@ struct DecodeParams {
     float *weights_copy;
     uint16_t *act;          /* [k, ffn] bf16 activations */
     k3_moe_expert *sel;     /* [k] descriptors of the selected experts */
+    uint16_t *y;            /* [k, hidden] bf16 per-slot expert outputs */
+    uint32_t *slot_mask;    /* bit s: slot s has an expert */
     uint32_t hidden, ffn, expert_count, top_k;
     float scale;
     uint32_t activation;

@@ -412,6 +412,45 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
 }
 
 /* ---------------------------------------------------------------------- */
+/* XCD-aware work order                                                    */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * Workgroups are dealt to the eight XCDs round robin by linear id, and each
+ * XCD has its own L2. Work item w = (tile, column block); XCD x takes the
+ * contiguous range [x per, (x + 1) per) of the works, ordered in groups of
+ * up to kGroupTiles consecutive tiles (the same expert, for heavy experts)
+ * with the tile fastest inside a column: the ~32 blocks an XCD runs at once
+ * then share about 4 activation tiles and 8 weight slices in that L2
+ * instead of fetching 32 different pairs through the fabric.
+ * Returns false for blocks beyond the work count.
+ */
+constexpr uint32_t kGroupTiles = 4u;
+
+__device__ __forceinline__ bool xcd_work(uint32_t ntiles, uint32_t cols, uint32_t &tile,
+                                         uint32_t &col) {
+    const uint32_t L = blockIdx.x;
+    const uint32_t works = ntiles * cols, per = (works + 7u) / 8u;
+    const uint32_t j = L >> 3;
+    const uint32_t w = (L & 7u) * per + j;
+    if (j >= per || w >= works) return false;
+    const uint32_t span = kGroupTiles * cols;
+    const uint32_t tg = w / span, rem = w % span;
+    const uint32_t left = ntiles - kGroupTiles * tg;
+    const uint32_t gsz = left < kGroupTiles ? left : kGroupTiles;
+    tile = kGroupTiles * tg + rem % gsz;
+    col = rem / gsz;
+    return true;
+}
+
+/* Blocks for up to `cap` tiles of `cols` column blocks: xcd_work needs
+ * 8 ceil(cap cols / 8). */
+inline uint32_t xcd_grid(uint32_t cap, uint32_t cols) {
+    const uint64_t works = (uint64_t)cap * cols;
+    return (uint32_t)(8u * ((works + 7u) / 8u));
+}
+
+/* ---------------------------------------------------------------------- */
 /* gate/up                                                                 */
 /* ---------------------------------------------------------------------- */
 
@@ -426,7 +465,7 @@ struct GateUpArgs {
 };
 
 /*
- * grid (F / (BN / 2), tile cap), block C::THREADS, LDS C::LDS bytes. The block's
+ * grid xcd_grid(tile cap, F / (BN / 2)), block C::THREADS. The block's
  * BN weight rows are BN / 2 gate rows and the same up rows: wave column wn
  * owns f-columns f0 + 8 WN wn .. + 8 WN, n-subtiles j < WN / 2 gate and
  * j >= WN / 2 up, so gate and up of a column meet in one lane. Epilogue:
@@ -436,8 +475,8 @@ struct GateUpArgs {
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
-    const uint32_t tile = blockIdx.y;
-    if (tile >= *A.tile_count) return;
+    uint32_t tile, colb;
+    if (!xcd_work(*A.tile_count, A.F / (uint32_t)(C::BN / 2), tile, colb)) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t wm = wave / C::NW, wn = wave % C::NW;
@@ -446,7 +485,7 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     const uint32_t H = A.H, F = A.F;
     const k3_moe_expert ex = A.experts[e];
     constexpr int FW = 8 * C::WN; /* f-columns per wave column */
-    const uint32_t f0 = blockIdx.x * (uint32_t)(C::BN / 2);
+    const uint32_t f0 = colb * (uint32_t)(C::BN / 2);
     /* weight row of block subtile J, lane row c: gate rows for the first
      * half of each wave column's subtiles, up rows (offset by F) after */
     auto wrow = [&](int J, uint32_t cc) -> uint32_t {
@@ -560,12 +599,12 @@ struct DownArgs {
     uint32_t H, F;
 };
 
-/* grid (H / BN, tile cap), block C::THREADS: y[route] rows d0 .. d0 + BN. */
+/* grid xcd_grid(tile cap, H / BN), block C::THREADS: y[route] rows d0 .. d0 + BN. */
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
-    const uint32_t tile = blockIdx.y;
-    if (tile >= *A.tile_count) return;
+    uint32_t tile, colb;
+    if (!xcd_work(*A.tile_count, A.H / (uint32_t)C::BN, tile, colb)) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t wm = wave / C::NW, wn = wave % C::NW;
@@ -573,7 +612,7 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     const uint32_t rows = A.tiles[3u * tile + 2u];
     const uint32_t H = A.H, F = A.F;
     const k3_moe_expert ex = A.experts[e];
-    const uint32_t d0 = blockIdx.x * (uint32_t)C::BN;
+    const uint32_t d0 = colb * (uint32_t)C::BN;
     const uint8_t *wp = (const uint8_t *)ex.down_packed, *ws = (const uint8_t *)ex.down_scales;
     auto prow = [&](uint32_t r) -> uint64_t { return (uint64_t)row0 + (r < rows ? r : 0u); };
     Loader<C> L;
@@ -633,13 +672,13 @@ using Cls2 = TileCfg<2, 4, 4, 4, TERMS, 3>; /* 8 waves: two per SIMD */
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C>), dim3(a.F / (C::BN / 2), cap),
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C>), dim3(xcd_grid(cap, a.F / (C::BN / 2))),
                        dim3(C::THREADS), 0, st, a);
 }
 
 template <class C>
 void launch_down(const DownArgs &a, uint32_t cap, hipStream_t st) {
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(a.H / C::BN, cap),
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(xcd_grid(cap, a.H / C::BN)),
                        dim3(C::THREADS), 0, st, a);
 }
 

@@ -81,7 +81,7 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
     w.counts = (uint32_t *)take(4ull * s.expert_count);
     w.offsets = (uint32_t *)take(4ull * (s.expert_count + 1u));
     w.unique = (uint32_t *)take(4ull * s.expert_count);
-    w.summary = (uint32_t *)take(16);
+    w.summary = (uint32_t *)take(16); /* [0..2] plan summary, [3] decode slot mask */
     w.token_index = (uint32_t *)take(4ull * routes);
     w.route_index = (uint32_t *)take(4ull * routes);
     w.chunk_base = (uint32_t *)take(plan_scratch(T, s.expert_count));
@@ -90,7 +90,7 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
     /* grouped path: every T > 1, and T == 1 when the decode kernels do not
      * cover the shape */
     const bool grouped = T > 1u || !decode_supported(s);
-    w.y = (uint16_t *)take(grouped ? 2ull * routes * s.hidden : 0u);
+    w.y = (uint16_t *)take(2ull * routes * s.hidden); /* per-slot expert outputs */
     if (grouped) {
         /* MFMA path: activation codes reuse `act` (two byte planes of the
          * bf16 activation's size) */
@@ -436,6 +436,8 @@ DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden
     P.weights_copy = (float *)w_copy;
     P.act = ws.act;
     P.sel = ws.sel;
+    P.y = ws.y;
+    P.slot_mask = ws.summary + 3;
     P.hidden = s.hidden;
     P.ffn = s.ffn;
     P.expert_count = s.expert_count;

@@ -100,6 +100,144 @@ bool launch_bf16_rows_f32(void *out, const void *w, const void *x, uint32_t toke
     return hipGetLastError() == hipSuccess;
 }
 
+/*
+ * The same w64 order for many tokens at once (router logits of a prefill
+ * batch), as a register-blocked GEMM: a block computes 32 tokens x 16 rows.
+ * Wave w (of 8) owns tokens 8 (w / 2) .. +8 and rows 8 (w % 2) .. +8; lane l
+ * keeps the 64 partial sums of its own chunks l, l + 64, ... -- exactly the
+ * per-lane partials of bf16_rows_f32_kernel -- and the wave64 butterfly of
+ * wave_sum_rows<64> finishes all 64 outputs at once, so the logits are
+ * bit-identical to the one-wave-per-row kernel.
+ *
+ * A K step covers 512 columns (64 chunks of 8). The step's bf16 tiles are
+ * loaded into registers one step ahead, then written to LDS as fp32 in two
+ * planes (elements 0-3 and 4-7 of each chunk), so every fragment read is a
+ * lane-contiguous ds_read_b128 and no conversion sits in the FMA loop.
+ * Out-of-range tokens/rows/chunks load zeros: fmaf(0, 0, acc) == acc
+ * for every acc the loop can hold (+0 + +0 = +0), so padding changes no bit.
+ *
+ * Block order is XCD-aware: workgroups are dealt to the eight XCDs round
+ * robin, and XCD x walks (token tile, its contiguous range of row tiles)
+ * with the row tiles fastest, so its 16-row weight slices stay in its own
+ * L2 and each token tile is fetched once per XCD.
+ */
+constexpr int kGT = 32, kGE = 16, kGThreads = 512;
+constexpr uint32_t kGemmMinTokens = 128;
+
+__global__ __launch_bounds__(512) void bf16_gemm_w64_kernel(
+        float *__restrict__ out, const uint16_t *__restrict__ weights,
+        const uint16_t *__restrict__ input, uint32_t tokens, uint32_t rows, uint32_t cols,
+        uint32_t row_tiles, uint32_t xcd_groups) {
+    __shared__ float4 xs[2][kGT][64];
+    __shared__ float4 wsm[2][kGE][64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    /* block -> (token tile, row tile) */
+    uint32_t tt, et;
+    {
+        const uint32_t L = blockIdx.x;
+        if (xcd_groups) {
+            const uint32_t x = L & 7u, j = L >> 3;
+            const uint32_t base = row_tiles >> 3, rem = row_tiles & 7u;
+            const uint32_t cnt = base + (x < rem ? 1u : 0u);
+            const uint32_t start = x * base + (x < rem ? x : rem);
+            const uint32_t token_tiles = (tokens + kGT - 1u) / kGT;
+            if (cnt == 0u || j >= token_tiles * cnt) return;
+            tt = j / cnt;
+            et = start + j % cnt;
+        } else {
+            tt = L / row_tiles;
+            et = L % row_tiles;
+        }
+    }
+    const uint32_t t0 = tt * kGT, e0 = et * kGE;
+    const uint32_t chunks = cols / 8u, nsteps = (chunks + 63u) / 64u;
+    const uint4 *x4 = (const uint4 *)input, *w4 = (const uint4 *)weights;
+    /* this thread's 6 staging items: items < 2048 are x (token i / 64,
+     * chunk i % 64), the rest weight rows */
+    constexpr int kItems = (kGT + kGE) * 64 / kGThreads;
+    uint4 reg[kItems];
+    auto load_step = [&](uint32_t s) {
+#pragma unroll
+        for (int q = 0; q < kItems; q++) {
+            const uint32_t it = tid + (uint32_t)q * kGThreads;
+            const uint32_t c = 64u * s + (it & 63u);
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (it < (uint32_t)kGT * 64u) {
+                const uint32_t t = t0 + (it >> 6);
+                if (t < tokens && c < chunks) v = x4[(uint64_t)t * chunks + c];
+            } else {
+                const uint32_t e = e0 + ((it >> 6) - (uint32_t)kGT);
+                if (e < rows && c < chunks) v = w4[(uint64_t)e * chunks + c];
+            }
+            reg[q] = v;
+        }
+    };
+    const uint32_t wt = wave >> 1, we = wave & 1u;
+    float acc[64];
+#pragma unroll
+    for (int i = 0; i < 64; i++) acc[i] = 0.0f;
+    load_step(0u);
+    for (uint32_t s = 0; s < nsteps; s++) {
+        __syncthreads(); /* the previous step's reads are done */
+#pragma unroll
+        for (int q = 0; q < kItems; q++) {
+            const uint32_t it = tid + (uint32_t)q * kGThreads;
+            const uint4 v = reg[q];
+            const float4 p0 = make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+            const float4 p1 = make_float4(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w));
+            const uint32_t r = it >> 6, c = it & 63u;
+            if (it < (uint32_t)kGT * 64u) {
+                xs[0][r][c] = p0;
+                xs[1][r][c] = p1;
+            } else {
+                wsm[0][r - kGT][c] = p0;
+                wsm[1][r - kGT][c] = p1;
+            }
+        }
+        __syncthreads();
+        if (s + 1u < nsteps) load_step(s + 1u);
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            float4 xv[8], wv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                xv[i] = xs[p][8u * wt + i][lane];
+                wv[i] = wsm[p][8u * we + i][lane];
+            }
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float a = acc[8 * t + e];
+                    a = fmaf(wv[e].x, xv[t].x, a);
+                    a = fmaf(wv[e].y, xv[t].y, a);
+                    a = fmaf(wv[e].z, xv[t].z, a);
+                    a = fmaf(wv[e].w, xv[t].w, a);
+                    acc[8 * t + e] = a;
+                }
+        }
+    }
+    const float v = wave_sum_rows<64>(acc);
+    const int owner = wave_rows_owner<64>();
+    const uint32_t t = t0 + 8u * wt + (uint32_t)(owner >> 3);
+    const uint32_t e = e0 + 8u * we + (uint32_t)(owner & 7);
+    if (t < tokens && e < rows) out[(uint64_t)t * rows + e] = v;
+}
+
+bool launch_bf16_gemm_w64(float *out, const void *w, const void *x, uint32_t tokens,
+                          uint32_t rows, uint32_t cols, hipStream_t s) {
+    const uint32_t token_tiles = (tokens + kGT - 1u) / kGT;
+    const uint32_t row_tiles = (rows + kGE - 1u) / kGE;
+    const uint32_t xcd = row_tiles >= 8u ? 1u : 0u;
+    const uint64_t blocks = xcd ? 8ull * token_tiles * ((row_tiles + 7u) / 8u)
+                                : (uint64_t)token_tiles * row_tiles;
+    if (blocks > 0x7fffffffull) return false;
+    hipLaunchKernelGGL(bf16_gemm_w64_kernel, dim3((uint32_t)blocks), dim3(kGThreads), 0, s, out,
+                       (const uint16_t *)w, (const uint16_t *)x, tokens, rows, cols, row_tiles,
+                       xcd);
+    return hipGetLastError() == hipSuccess;
+}
+
 /* ------------------------------------------------------------------------ */
 /* router top-k                                                              */
 /* ------------------------------------------------------------------------ */
@@ -262,6 +400,9 @@ bool k3::launch_bf16_rows_f32_any(float *out, const void *w, const void *x, uint
                                   uint32_t rows, uint32_t cols, hipStream_t s) {
     if (tokens == 1u) return launch_bf16_rows_f32<1>(out, w, x, 1u, rows, cols, s);
     if (tokens <= 4u) return launch_bf16_rows_f32<4>(out, w, x, tokens, rows, cols, s);
+    /* many tokens: the blocked GEMM (same bits); it needs 16-byte rows */
+    if (tokens >= kGemmMinTokens && cols % 8u == 0u && ((uintptr_t)w | (uintptr_t)x) % 16u == 0u)
+        return launch_bf16_gemm_w64(out, w, x, tokens, rows, cols, s);
     return launch_bf16_rows_f32<16>(out, w, x, tokens, rows, cols, s);
 }
 

@@ -53,8 +53,9 @@ __device__ __forceinline__ void wave_fence() {
 /* key[j]/score[j] for expert lane + 64 j. Writes ids/weights[0..top_k) (and
  * the optional copies, which may be host-mapped). Must be called by all 64
  * lanes of the wave; top_k <= 32. With `publish`, ids/weights are written
- * with write-through agent-scope stores (for readers in the same kernel). */
-__device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlots],
+ * with write-through agent-scope stores (for readers in the same kernel).
+ * Returns the rank-`lane` id to lanes < top_k (UINT32_MAX elsewhere). */
+__device__ __forceinline__ uint32_t topk_select_wave(const uint32_t (&key)[kTopkSlots],
                                                  const float (&score)[kTopkSlots],
                                                  uint32_t top_k, float scale, uint32_t *ids,
                                                  float *weights, uint32_t *ids_copy,
@@ -124,8 +125,9 @@ __device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlot
     for (uint32_t q = 0; q < top_k; q++)
         den = __fadd_rn(den, __builtin_bit_cast(float, __builtin_amdgcn_readlane(
                                  __builtin_bit_cast(int, my_score), (int)q)));
+    uint32_t id = UINT32_MAX;
     if (lane < top_k) {
-        const uint32_t id = lane < nsel ? sm.out_id[lane] : UINT32_MAX;
+        id = lane < nsel ? sm.out_id[lane] : UINT32_MAX;
         const float wr = __fmul_rn(__fdiv_rn(my_score, den), scale);
         if (publish) {
             __hip_atomic_store(ids + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -137,6 +139,7 @@ __device__ __forceinline__ void topk_select_wave(const uint32_t (&key)[kTopkSlot
         if (ids_copy) ids_copy[lane] = id;
         if (w_copy) w_copy[lane] = wr;
     }
+    return id;
 }
 
 }  // namespace k3

@@ -121,7 +121,12 @@ def test_mxfp4_misaligned_8mod16(cuda):
     np.testing.assert_array_equal(host(out).view(np.uint16), want[0])
 
 
-@pytest.mark.parametrize("T,E,H", [(1, 896, 7168), (3, 64, 2048), (17, 896, 7168), (4, 100, 1001)])
+@pytest.mark.parametrize("T,E,H", [(1, 896, 7168), (3, 64, 2048), (17, 896, 7168), (4, 100, 1001),
+                                   # blocked-GEMM path (T >= 128): ragged token/row tiles,
+                                   # a partial last K step (65 chunks), XCD grouping with a
+                                   # remainder (9 row tiles) and without (7 row tiles)
+                                   (300, 896, 7168), (129, 100, 520), (1000, 137, 1024),
+                                   (128, 16, 8)])
 def test_router_logits_bitexact(cuda, T, E, H):
     rng = np.random.default_rng(E + H + T)
     w = rand_bf16(rng, (E, H), 0.02)
