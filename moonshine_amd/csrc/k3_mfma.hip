@@ -140,18 +140,35 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
 /*
  * Block tile: MW x NW waves; wave tile (16 WM activation rows) x (16 WN
  * weight rows). Per K step of 128 the block stages in LDS
- *   A   TERMS x (BM / 16) x 2 chunks of 1 KB: chunk (t, i, h) holds, in lane
- *       order, the 16 bytes lane l supplies for half h of its FP8 fragment of
- *       row 16 i + l % 16 (bytes 64 h + 16 (l / 16) of the step);
+ *   A   TERMS x (BM / 16) x 2 chunks of 1 KB: chunk (t, i, h) holds the
+ *       step's full 128 bytes of the 8 rows 16 i + 8 h + r (r < 8), slot
+ *       8 r + q' holding 16-byte piece p = q' ^ a_swizzle(r, h) -- one
+ *       instruction fetches eight whole 128-byte lines;
  *   B   BN / 16 chunks of 1 KB: lane order FP4 fragments of 16 rows;
  *   SA  TERMS x max(BM, 64) dwords: the 4 E8M0 bytes of each row's step;
  *   SB  BN dwords.
  * Every chunk is written by one global_load_lds instruction (lane l's 16 or
- * 4 bytes land at chunk + 16 l or + 4 l), so fragments are read back with
- * conflict-free ds_read_b128 at lane * 16. Chunks are dealt to the four
- * waves in equal numbers per kind; the A scale chunks of small tiles (fewer
- * than four) go to the first waves.
+ * 4 bytes land at chunk + 16 l or + 4 l). B fragments are read back with
+ * ds_read_b128 at lane * 16; an A fragment (row c, pieces g and 4 + g) is
+ * read at the swizzled slot, which puts the 16 lanes of each read pass on
+ * 16 different 16-byte bank groups. Chunks are dealt to the waves in equal
+ * numbers per kind; the A scale chunks of small tiles (fewer than the
+ * waves) go to the first waves.
  */
+/* XOR swizzle of the 16-byte pieces of row r of A chunk half h. */
+__device__ __forceinline__ uint32_t a_swizzle(uint32_t r, uint32_t h) {
+    return (r >> 1) | (h << 2);
+}
+/* Byte offset, inside a chunk pair (t, i), of 16-byte piece p of row c. */
+__device__ __forceinline__ uint32_t a_slot(uint32_t c, uint32_t p) {
+    const uint32_t h = c >> 3, r = c & 7u;
+    return 1024u * h + 128u * r + 16u * (p ^ a_swizzle(r, h));
+}
+/* Row (within the chunk pair) and source piece of lane L of chunk half h. */
+__device__ __forceinline__ uint32_t a_dma_row(uint32_t L, uint32_t h) { return 8u * h + (L >> 3); }
+__device__ __forceinline__ uint32_t a_dma_piece(uint32_t L, uint32_t h) {
+    return (L & 7u) ^ a_swizzle(L >> 3, h);
+}
 /* How the chunks of one kind are dealt to the block's W waves: N >= W
  * chunks must split evenly (wave w takes w, w + W, ...); fewer go one each
  * to the first N waves. */
@@ -314,7 +331,8 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t base = lds_addr(st);
-    const uint32_t a_base = base + 16u * lane + 2048u * C::WM * wm;
+    const uint32_t a_lo = base + a_slot(c, g) + 2048u * C::WM * wm;
+    const uint32_t a_hi = base + a_slot(c, 4u + g) + 2048u * C::WM * wm;
     const uint32_t b_base = base + 16u * lane + 1024u * C::WN * wn;
     const uint32_t sa_base = base + 4u * c + 64u * C::WM * wm;
     const uint32_t sb_base = base + 4u * c + 64u * C::WN * wn;
@@ -323,8 +341,8 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     static_for<C::TERMS * C::WM>([&](auto I) {
         constexpr int t = decltype(I)::value / C::WM, i = decltype(I)::value % C::WM;
         constexpr int off = C::OFF_A + 2048 * (t * (C::BM / 16) + i);
-        alo[t][i] = ds_read16<off>(a_base);
-        ahi[t][i] = ds_read16<off + 1024>(a_base);
+        alo[t][i] = ds_read16<off>(a_lo);
+        ahi[t][i] = ds_read16<off>(a_hi);
         saw[t][i] = ds_read4<C::OFF_SA + 4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
     });
     static_for<C::WN>([&](auto J) {
@@ -520,7 +538,7 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
         for (int q = 0; q < C::DA::per; q++) {
             const int ch = min(chunk_of<typename C::DA, W>(q, wave), C::A_CH - 1);
             const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
-            L.a[q] = a_row(t, 16u * i + c) + 64u * h + 16u * g;
+            L.a[q] = a_row(t, 16u * i + a_dma_row(lane, h)) + 16u * a_dma_piece(lane, h);
         }
 #pragma unroll
         for (int q = 0; q < C::DB::per; q++) {
@@ -622,7 +640,7 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     for (int q = 0; q < C::DA::per; q++) {
         const int ch = min(chunk_of<typename C::DA, W>(q, wave), C::A_CH - 1);
         const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
-        L.a[q] = A.B.aq[t] + prow(16u * i + c) * F + 64u * h + 16u * g;
+        L.a[q] = A.B.aq[t] + prow(16u * i + a_dma_row(lane, h)) * F + 16u * a_dma_piece(lane, h);
     }
 #pragma unroll
     for (int q = 0; q < C::DB::per; q++) {
