@@ -266,7 +266,10 @@ def main():
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (C oracle) ...")
         threads = min(len(os.sched_getaffinity(0)), 16)
-        cpu_inputs = make_inputs(cfg, tokens=min(T, 64))
+        # a bounded sample of the same workload: up to 64 tokens (the first
+        # rows of the seeded batch; for T = 1 the rotated decode tokens),
+        # each run through the oracle layer as its own token
+        cpu_inputs = make_inputs(cfg, tokens=64)
         result["cpu_baseline"] = cpu_baseline(cfg, cpu_inputs, moe.store, args.cpu_budget,
                                               threads)
     print(json.dumps(result), flush=True)
