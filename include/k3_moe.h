@@ -120,7 +120,9 @@ bool k3_moe_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
  * residual may be NULL (output is then the combine alone). experts is a
  * DEVICE array of expert_count descriptors. expert_ids / expert_weights
  * ([T, k] u32 / f32) are optional extra copies of the routes and may be
- * host-mapped memory. token_count <= 65535.
+ * host-mapped memory. token_count <= 65535. output, hidden and residual
+ * rows are read and written 16 bytes at a time: the three pointers must
+ * be 16-byte aligned (false otherwise).
  */
 bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
                          const void *router_weight, const void *router_bias,
@@ -143,8 +145,8 @@ enum {
     K3_MOE_STAGE_TOPK = 1,     /* top-k + route weights */
     K3_MOE_STAGE_PLAN = 2,     /* routing plan (T > 1) */
     K3_MOE_STAGE_GATE_UP = 3,  /* gate/up products + activation */
-    K3_MOE_STAGE_DOWN = 4,     /* down products (T = 1: + combine + residual) */
-    K3_MOE_STAGE_COMBINE = 5,  /* weighted combine + residual (T > 1) */
+    K3_MOE_STAGE_DOWN = 4,     /* down products, one bf16 row per route */
+    K3_MOE_STAGE_COMBINE = 5,  /* weighted combine + residual */
     K3_MOE_STAGE_END = 6,
     K3_MOE_STAGE_COUNT = 7,
 };
@@ -167,7 +169,8 @@ bool k3_moe_forward_profiled_bf16(void *output, const void *hidden,
 /*
  * Expert stage only, on routes computed elsewhere (ids/weights [T, k] on
  * the device): lets the engine keep its own router, and lets tests check
- * the expert products on identical routes.
+ * the expert products on identical routes. Alignment as for
+ * k3_moe_forward_bf16.
  */
 bool k3_moe_experts_bf16(void *output, const void *hidden, const void *residual,
                          const void *expert_ids, const void *expert_weights,

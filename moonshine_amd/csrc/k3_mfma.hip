@@ -324,10 +324,25 @@ __device__ __forceinline__ void after_wait(T &v) {
     asm volatile("" : "+v"(v));
 }
 
-/* One K step from a staged LDS buffer: fragments, then the MFMAs. */
+/* s_waitcnt lgkmcnt(N) (N < 16), other counters untouched. */
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (N << 8) | (3 << 14));
+}
+
+/*
+ * One K step from a staged LDS buffer. The (term, row-block) fragment list
+ * is read in two halves: the B fragments and the first half of the A
+ * fragments, then the second half; the first half's MFMAs are issued as
+ * soon as its reads have landed (lgkmcnt(count of the second half's
+ * reads)), so the second half's LDS reads run under them.
+ */
 template <class C>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
                                           uint32_t wm, uint32_t wn) {
+    constexpr int NA = C::TERMS * C::WM, H1 = (NA + 1) / 2, H2 = NA - H1;
+    static_assert(3 * H2 < 16, "second-half reads fit the lgkm counter");
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t base = lds_addr(st);
@@ -336,60 +351,56 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     const uint32_t b_base = base + 16u * lane + 1024u * C::WN * wn;
     const uint32_t sa_base = base + 4u * c + 64u * C::WM * wm;
     const uint32_t sb_base = base + 4u * c + 64u * C::WN * wn;
-    u32x4_t alo[C::TERMS][C::WM], ahi[C::TERMS][C::WM], bv[C::WN];
-    uint32_t saw[C::TERMS][C::WM], sbw[C::WN];
-    static_for<C::TERMS * C::WM>([&](auto I) {
-        constexpr int t = decltype(I)::value / C::WM, i = decltype(I)::value % C::WM;
+    u32x4_t alo[NA], ahi[NA], bv[C::WN];
+    uint32_t saw[NA], sbw[C::WN];
+    auto read_a = [&](auto I) {
+        constexpr int q = decltype(I)::value, t = q / C::WM, i = q % C::WM;
         constexpr int off = C::OFF_A + 2048 * (t * (C::BM / 16) + i);
-        alo[t][i] = ds_read16<off>(a_lo);
-        ahi[t][i] = ds_read16<off>(a_hi);
-        saw[t][i] = ds_read4<C::OFF_SA + 4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
-    });
+        alo[q] = ds_read16<off>(a_lo);
+        ahi[q] = ds_read16<off>(a_hi);
+        saw[q] = ds_read4<C::OFF_SA + 4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
+    };
     static_for<C::WN>([&](auto J) {
         constexpr int j = decltype(J)::value;
         bv[j] = ds_read16<C::OFF_B + 1024 * j>(b_base);
         sbw[j] = ds_read4<C::OFF_SB + 64 * j>(sb_base);
     });
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int t = 0; t < C::TERMS; t++)
-#pragma unroll
-        for (int i = 0; i < C::WM; i++) {
-            after_wait(alo[t][i]);
-            after_wait(ahi[t][i]);
-            after_wait(saw[t][i]);
-        }
-#pragma unroll
-    for (int j = 0; j < C::WN; j++) {
-        after_wait(bv[j]);
-        after_wait(sbw[j]);
-    }
-    i32x8 af[C::TERMS][C::WM];
-    int sa[C::TERMS][C::WM];
-#pragma unroll
-    for (int t = 0; t < C::TERMS; t++)
-#pragma unroll
-        for (int i = 0; i < C::WM; i++) {
-            af[t][i] = i32x8{(int)alo[t][i].x, (int)alo[t][i].y, (int)alo[t][i].z,
-                             (int)alo[t][i].w, (int)ahi[t][i].x, (int)ahi[t][i].y,
-                             (int)ahi[t][i].z, (int)ahi[t][i].w};
-            sa[t][i] = (int)((saw[t][i] >> (8u * g)) & 255u);
-        }
-    i32x8 bf[C::WN];
-    int sb[C::WN];
-#pragma unroll
-    for (int j = 0; j < C::WN; j++) {
-        bf[j] = i32x8{(int)bv[j].x, (int)bv[j].y, (int)bv[j].z, (int)bv[j].w, 0, 0, 0, 0};
-        sb[j] = (int)((sbw[j] >> (8u * g)) & 255u);
-    }
-#pragma unroll
-    for (int t = 0; t < C::TERMS; t++)
-#pragma unroll
-        for (int i = 0; i < C::WM; i++)
-#pragma unroll
-            for (int j = 0; j < C::WN; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    af[t][i], bf[j], acc[i][j], 0, 4, 0, sa[t][i], 0, sb[j]);
+    static_for<H1>([&](auto I) { read_a(I); });
+    static_for<H2>([&](auto I) { read_a(std::integral_constant<int, H1 + decltype(I)::value>{}); });
+    auto mfmas = [&](auto Q) {
+        constexpr int q = decltype(Q)::value, i = q % C::WM;
+        const i32x8 af = i32x8{(int)alo[q].x, (int)alo[q].y, (int)alo[q].z, (int)alo[q].w,
+                               (int)ahi[q].x, (int)ahi[q].y, (int)ahi[q].z, (int)ahi[q].w};
+        const int sa = (int)((saw[q] >> (8u * g)) & 255u);
+        static_for<C::WN>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const i32x8 bf = i32x8{(int)bv[j].x, (int)bv[j].y, (int)bv[j].z, (int)bv[j].w, 0, 0, 0, 0};
+            const int sb = (int)((sbw[j] >> (8u * g)) & 255u);
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf, acc[i][j], 0, 4, 0,
+                                                                         sa, 0, sb);
+        });
+    };
+    /* first half (and B) landed */
+    wait_lgkm<3 * H2>();
+    static_for<C::WN>([&](auto J) {
+        after_wait(bv[decltype(J)::value]);
+        after_wait(sbw[decltype(J)::value]);
+    });
+    static_for<H1>([&](auto I) {
+        after_wait(alo[decltype(I)::value]);
+        after_wait(ahi[decltype(I)::value]);
+        after_wait(saw[decltype(I)::value]);
+    });
+    static_for<H1>([&](auto I) { mfmas(I); });
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkm<0>();
+    static_for<H2>([&](auto I) {
+        constexpr int q = H1 + decltype(I)::value;
+        after_wait(alo[q]);
+        after_wait(ahi[q]);
+        after_wait(saw[q]);
+    });
+    static_for<H2>([&](auto I) { mfmas(std::integral_constant<int, H1 + decltype(I)::value>{}); });
 }
 
 /* Step s of the ring: wait for this wave's loads of step s (one later step

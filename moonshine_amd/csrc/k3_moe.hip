@@ -362,23 +362,57 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
 }
 
 /* out[t, d] = bf16(residual + bf16(sum_r w[t, r] * y[t*k + r, d])), rank
- * order, invalid routes skipped. */
-__global__ __launch_bounds__(256) void combine_kernel(
+ * order, invalid routes skipped (k3_rocm_ops.cu:1452-1510). grid
+ * (ceil(H / (8 * 128)), T), block 128: a thread owns 8 consecutive d (one
+ * 16-byte load per route); every load is issued before the first use, so
+ * a token costs one memory round trip. H % 8 == 0, rows 16-byte aligned. */
+constexpr uint32_t kCombineThreads = 128;
+
+__global__ __launch_bounds__(128) void combine_kernel(
         uint16_t *__restrict__ out, const uint16_t *__restrict__ y,
         const uint16_t *__restrict__ residual, const uint32_t *__restrict__ ids,
         const float *__restrict__ wts, uint32_t H, uint32_t k, uint32_t E) {
     const uint32_t t = blockIdx.y;
-    for (uint32_t d = blockIdx.x * blockDim.x + threadIdx.x; d < H; d += blockDim.x * gridDim.x) {
-        float c = 0.0f;
-        for (uint32_t r = 0; r < k; r++) {
-            const uint64_t route = (uint64_t)t * k + r;
-            if (ids[route] < E)
-                c = __fadd_rn(c, __fmul_rn(wts[route], bf16_to_f32(y[route * H + d])));
-        }
-        const float cb = bf16_round(c);
-        const uint64_t o = (uint64_t)t * H + d;
-        out[o] = residual ? f32_to_bf16(__fadd_rn(bf16_to_f32(residual[o]), cb)) : f32_to_bf16(cb);
+    const uint32_t d = 8u * (blockIdx.x * kCombineThreads + threadIdx.x);
+    if (d >= H) return;
+    const uint64_t r0 = (uint64_t)t * k;
+    uint4 yv[32];
+    float w[32];
+    bool live[32];
+#pragma unroll
+    for (int r = 0; r < 32; r++) { /* route 0 stands in for r >= k */
+        const uint64_t route = r0 + ((uint32_t)r < k ? (uint32_t)r : 0u);
+        yv[r] = *(const uint4 *)(y + route * H + d);
+        w[r] = wts[route];
+        live[r] = ((uint32_t)r < k) & (ids[route] < E);
     }
+    const uint64_t o = (uint64_t)t * H + d;
+    const uint4 rv = residual ? *(const uint4 *)(residual + o) : make_uint4(0u, 0u, 0u, 0u);
+    float c[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) c[i] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+        if (!live[r]) continue;
+        const uint32_t u[4] = {yv[r].x, yv[r].y, yv[r].z, yv[r].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            c[2 * q] = __fadd_rn(c[2 * q], __fmul_rn(w[r], bf16_lo(u[q])));
+            c[2 * q + 1] = __fadd_rn(c[2 * q + 1], __fmul_rn(w[r], bf16_hi(u[q])));
+        }
+    }
+    const uint32_t ru[4] = {rv.x, rv.y, rv.z, rv.w};
+    uint32_t ov[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        uint32_t lo = f32_to_bf16(bf16_round(c[2 * q])), hi = f32_to_bf16(bf16_round(c[2 * q + 1]));
+        if (residual) {
+            lo = f32_to_bf16(__fadd_rn(bf16_lo(ru[q]), bf16_round(c[2 * q])));
+            hi = f32_to_bf16(__fadd_rn(bf16_hi(ru[q]), bf16_round(c[2 * q + 1])));
+        }
+        ov[q] = lo | (hi << 16);
+    }
+    *(uint4 *)(out + o) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -399,6 +433,11 @@ __global__ void synth_fill_kernel(uint8_t *__restrict__ base, uint64_t bytes, ui
         for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes; i += stride)
             base[i] = synth_byte(key, i, 1u);
     }
+}
+
+/* output, hidden and residual (nullable) rows move in 16-byte pieces. */
+bool rows_aligned(const void *output, const void *hidden, const void *residual) {
+    return (((uintptr_t)output | (uintptr_t)hidden | (uintptr_t)residual) % 16u) == 0u;
 }
 
 bool shape_ok(const k3_moe_shape *s) {
@@ -471,9 +510,9 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
                                  precision == K3_MOE_MFMA ? 2u : 1u, st, mark))
             return false;
         mark(K3_MOE_STAGE_COMBINE);
-        hipLaunchKernelGGL(combine_kernel, dim3((H + 255u) / 256u, T), dim3(256), 0, st,
-                           (uint16_t *)output, ws.y, (const uint16_t *)residual, ws.ids,
-                           ws.weights, H, k, E);
+        hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
+                           dim3(kCombineThreads), 0, st, (uint16_t *)output, ws.y,
+                           (const uint16_t *)residual, ws.ids, ws.weights, H, k, E);
         mark(K3_MOE_STAGE_END);
         return hipGetLastError() == hipSuccess;
     }
@@ -489,9 +528,9 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
                        dim3(256), 0, st, ws.y, ws.act, ws.unique, ws.summary, ws.counts,
                        ws.offsets, ws.route_index, experts, H, F);
     mark(K3_MOE_STAGE_COMBINE);
-    hipLaunchKernelGGL(combine_kernel, dim3((H + 255u) / 256u, T), dim3(256), 0, st,
-                       (uint16_t *)output, ws.y, (const uint16_t *)residual, ws.ids, ws.weights,
-                       H, k, E);
+    hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
+                       dim3(kCombineThreads), 0, st, (uint16_t *)output, ws.y,
+                       (const uint16_t *)residual, ws.ids, ws.weights, H, k, E);
     mark(K3_MOE_STAGE_END);
     return hipGetLastError() == hipSuccess;
 }
@@ -538,7 +577,7 @@ extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void
                                     uint32_t token_count, uint32_t precision, void *workspace,
                                     size_t workspace_bytes, void *stream) {
     if (!output || !hidden || !expert_ids || !expert_weights || !experts || !workspace ||
-        !precision_ok(shape, token_count, precision))
+        !precision_ok(shape, token_count, precision) || !rows_aligned(output, hidden, residual))
         return false;
     Workspace ws = carve(workspace, *shape, token_count);
     if (workspace_bytes < ws.bytes) return false;
@@ -560,7 +599,7 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
                                     size_t workspace_bytes, const k3_moe_profile *profile,
                                     void *stream) {
     if (!output || !hidden || !router_weight || !router_bias || !experts || !workspace ||
-        !precision_ok(shape, token_count, precision) || ((uintptr_t)hidden % 16u) != 0u)
+        !precision_ok(shape, token_count, precision) || !rows_aligned(output, hidden, residual))
         return false;
     Workspace ws = carve(workspace, *shape, token_count);
     if (workspace_bytes < ws.bytes) return false;

@@ -64,3 +64,17 @@ def test_workspace_sizes_and_validation():
                                      None)
     assert not L.k3_rocm_mxfp4_gemv_bf16(None, None, None, None, 16, 64, None)
     assert not L.k3_moe_mx8_quantize_bf16(None, None, None, None, None, 32, None)
+
+
+def test_row_alignment_is_validated_before_launch():
+    """output / hidden / residual rows move 16 bytes at a time: a pointer
+    that is not 16-byte aligned is refused (false, nothing launched)."""
+    L = _lib.lib()
+    s = ctypes.byref(shape(CONFIGS[1]))
+    buf = (ctypes.c_uint8 * 4096)()
+    base = (ctypes.addressof(buf) + 255) & ~255
+    ok, off = ctypes.c_void_p(base), ctypes.c_void_p(base + 8)
+    for out, hid, res in ((off, ok, ok), (ok, off, ok), (ok, ok, off)):
+        assert not L.k3_moe_forward_bf16(out, hid, res, ok, ok, ok, s, 1, 0, None, None, ok,
+                                         1 << 40, None)
+        assert not L.k3_moe_experts_bf16(out, hid, res, ok, ok, ok, s, 1, 0, ok, 1 << 40, None)
