@@ -190,6 +190,9 @@ struct TileCfg {
     static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, OFF_SA = OFF_B + B_CH * 1024;
     static constexpr int OFF_SB = OFF_SA + SA_CH * 256, STAGE = OFF_SB + SB_CH * 256;
     static constexpr int LDS = STAGE * STAGES;
+    /* two-stage (register-bound) tiles read the second half of their A
+     * fragments after the first half's MFMAs */
+    static constexpr bool SEQ = STAGES == 2;
     using DA = Deal<A_CH, NWV>;
     using DB = Deal<B_CH, NWV>;
     using DSA = Deal<SA_CH, NWV>;
@@ -348,9 +351,10 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     const uint32_t base = lds_addr(st);
     const uint32_t a_lo = base + a_slot(c, g) + 2048u * C::WM * wm;
     const uint32_t a_hi = base + a_slot(c, 4u + g) + 2048u * C::WM * wm;
-    const uint32_t b_base = base + 16u * lane + 1024u * C::WN * wn;
-    const uint32_t sa_base = base + 4u * c + 64u * C::WM * wm;
-    const uint32_t sb_base = base + 4u * c + 64u * C::WN * wn;
+    /* region bases in the address registers keep the immediates 16-bit */
+    const uint32_t b_base = base + C::OFF_B + 16u * lane + 1024u * C::WN * wn;
+    const uint32_t sa_base = base + C::OFF_SA + 4u * c + 64u * C::WM * wm;
+    const uint32_t sb_base = base + C::OFF_SB + 4u * c + 64u * C::WN * wn;
     u32x4_t alo[NA], ahi[NA], bv[C::WN];
     uint32_t saw[NA], sbw[C::WN];
     auto read_a = [&](auto I) {
@@ -358,15 +362,8 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
         constexpr int off = C::OFF_A + 2048 * (t * (C::BM / 16) + i);
         alo[q] = ds_read16<off>(a_lo);
         ahi[q] = ds_read16<off>(a_hi);
-        saw[q] = ds_read4<C::OFF_SA + 4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
+        saw[q] = ds_read4<4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
     };
-    static_for<C::WN>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        bv[j] = ds_read16<C::OFF_B + 1024 * j>(b_base);
-        sbw[j] = ds_read4<C::OFF_SB + 64 * j>(sb_base);
-    });
-    static_for<H1>([&](auto I) { read_a(I); });
-    static_for<H2>([&](auto I) { read_a(std::integral_constant<int, H1 + decltype(I)::value>{}); });
     auto mfmas = [&](auto Q) {
         constexpr int q = decltype(Q)::value, i = q % C::WM;
         const i32x8 af = i32x8{(int)alo[q].x, (int)alo[q].y, (int)alo[q].z, (int)alo[q].w,
@@ -380,6 +377,40 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
                                                                          sa, 0, sb);
         });
     };
+    static_for<C::WN>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        bv[j] = ds_read16<1024 * j>(b_base);
+        sbw[j] = ds_read4<64 * j>(sb_base);
+    });
+    if constexpr (C::SEQ) {
+        /* register-bound tiles: the second half's fragments are read into
+         * the registers the first half frees, after its MFMAs are issued */
+        static_for<H1>([&](auto I) { read_a(I); });
+        wait_lgkm<0>();
+        static_for<C::WN>([&](auto J) {
+            after_wait(bv[decltype(J)::value]);
+            after_wait(sbw[decltype(J)::value]);
+        });
+        static_for<H1>([&](auto I) {
+            after_wait(alo[decltype(I)::value]);
+            after_wait(ahi[decltype(I)::value]);
+            after_wait(saw[decltype(I)::value]);
+        });
+        static_for<H1>([&](auto I) { mfmas(I); });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<H2>([&](auto I) { read_a(std::integral_constant<int, H1 + decltype(I)::value>{}); });
+        wait_lgkm<0>();
+        static_for<H2>([&](auto I) {
+            constexpr int q = H1 + decltype(I)::value;
+            after_wait(alo[q]);
+            after_wait(ahi[q]);
+            after_wait(saw[q]);
+        });
+        static_for<H2>([&](auto I) { mfmas(std::integral_constant<int, H1 + decltype(I)::value>{}); });
+        return;
+    }
+    static_for<H1>([&](auto I) { read_a(I); });
+    static_for<H2>([&](auto I) { read_a(std::integral_constant<int, H1 + decltype(I)::value>{}); });
     /* first half (and B) landed */
     wait_lgkm<3 * H2>();
     static_for<C::WN>([&](auto J) {
@@ -428,9 +459,26 @@ template <class C>
 __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
                                               uint8_t *b0, uint8_t *b1, uint8_t *b2, uint32_t K,
                                               uint32_t wm, uint32_t wn) {
-    static_assert(C::STAGES == 3, "three buffers");
+    static_assert(C::STAGES == 2 || C::STAGES == 3, "two or three buffers");
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nsteps = K / 128u;
+    if constexpr (C::STAGES == 2) {
+        /* Two buffers, for tiles whose stage is too big for three: the
+         * step is long (one wave per SIMD, WM x WN x TERMS MFMAs each), so
+         * issuing step s + 1's loads at the start of step s hides them. */
+        auto step2 = [&](uint32_t s, const uint8_t *cur, uint8_t *nxt) __attribute__((always_inline)) {
+            wait_vm<0>();
+            __builtin_amdgcn_s_barrier();
+            if (s + 1u < nsteps) issue_step<C>(L, nxt, s + 1u, wave);
+            mfma_step<C>(acc, cur, wm, wn);
+        };
+        issue_step<C>(L, b0, 0u, wave);
+        for (uint32_t s = 0; s < nsteps; s += 2u) {
+            step2(s, b0, b1);
+            if (s + 1u < nsteps) step2(s + 1u, b1, b0);
+        }
+        return;
+    }
     issue_step<C>(L, b0, 0u, wave);
     if (nsteps > 1u) issue_step<C>(L, b1, 1u, wave);
     for (uint32_t s = 0; s < nsteps; s += 3u) {
@@ -503,7 +551,8 @@ struct GateUpArgs {
  */
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t b2[C::STAGES == 3 ? C::STAGE : 16];
     uint32_t tile, colb;
     if (!xcd_work(*A.tile_count, A.F / (uint32_t)(C::BN / 2), tile, colb)) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -631,7 +680,8 @@ struct DownArgs {
 /* grid xcd_grid(tile cap, H / BN), block C::THREADS: y[route] rows d0 .. d0 + BN. */
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE], b2[C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t b2[C::STAGES == 3 ? C::STAGE : 16];
     uint32_t tile, colb;
     if (!xcd_work(*A.tile_count, A.H / (uint32_t)C::BN, tile, colb)) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -696,8 +746,11 @@ template <int TERMS>
 using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3>;
 template <int TERMS>
 using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 3>;
+/* 128 x 512 blocks: four waves, one per SIMD, each 64 activation rows x
+ * 256 weight rows (accumulators in AGPRs); halves the activation re-reads
+ * of a 256-wide block, two stage buffers */
 template <int TERMS>
-using Cls2 = TileCfg<2, 4, 4, 4, TERMS, 3>; /* 8 waves: two per SIMD */
+using Cls2 = TileCfg<2, 4, 4, 8, TERMS, 2>;
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
@@ -762,7 +815,7 @@ void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[3]) {
 }
 
 bool mfma_supported(const k3_moe_shape &s) {
-    return s.hidden % 256u == 0u && s.ffn % 128u == 0u && s.expert_count <= 1024u;
+    return s.hidden % 512u == 0u && s.ffn % 256u == 0u && s.expert_count <= 1024u;
 }
 
 bool mfma_launch_experts(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
