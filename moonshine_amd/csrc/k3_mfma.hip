@@ -179,20 +179,26 @@ struct Deal {
     static_assert(partial || N % W == 0, "chunks split evenly over the waves");
 };
 
-template <int MW_, int NW_, int WM_, int WN_, int TERMS_, int STAGES_>
+template <int MW_, int NW_, int WM_, int WN_, int TERMS_, int STAGES_, int KS_ = 1>
 struct TileCfg {
     static constexpr int MW = MW_, NW = NW_, WM = WM_, WN = WN_, TERMS = TERMS_;
     static constexpr int STAGES = STAGES_, NWV = MW * NW, THREADS = 64 * NWV;
+    /* KS: 128-column K slices per stage. With KS = 2 a stage holds 128
+     * bytes of every weight row, so B chunks are whole 128-byte lines too
+     * (8 rows each, the A layout); KS = 1 keeps the 16-row lane-order
+     * fragments of 64 bytes per row. */
+    static constexpr int KS = KS_, KSTEP = 128 * KS;
     static constexpr int BM = MW * 16 * WM, BN = NW * 16 * WN;
-    static constexpr int A_CH = TERMS * (BM / 16) * 2, B_CH = BN / 16;
+    static constexpr int A_CH = KS * TERMS * (BM / 16) * 2, B_CH = KS == 2 ? BN / 8 : BN / 16;
     static constexpr int SA_ROWS = BM < 64 ? 64 : BM;
-    static constexpr int SA_CH = TERMS * SA_ROWS / 64, SB_CH = BN / 64;
+    static constexpr int SA_CH = KS * TERMS * SA_ROWS / 64, SB_CH = KS * BN / 64;
     static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, OFF_SA = OFF_B + B_CH * 1024;
     static constexpr int OFF_SB = OFF_SA + SA_CH * 256, STAGE = OFF_SB + SB_CH * 256;
     static constexpr int LDS = STAGE * STAGES;
-    /* two-stage (register-bound) tiles read the second half of their A
+    /* two waves per SIMD (register-bound) read the second half of their A
      * fragments after the first half's MFMAs */
-    static constexpr bool SEQ = STAGES == 2;
+    static constexpr bool SEQ = NWV > 4;
+    static_assert(KS == 1 || KS == 2, "one or two K slices per stage");
     using DA = Deal<A_CH, NWV>;
     using DB = Deal<B_CH, NWV>;
     using DSA = Deal<SA_CH, NWV>;
@@ -255,22 +261,22 @@ __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, u
     if (L.mask & 8u) {
 #pragma unroll
         for (int q = 0; q < C::DA::per; q++)
-            dma<16>(L.a[q] + 128u * s, stage + C::OFF_A + 1024 * chunk_of<typename C::DA, W>(q, wave));
+            dma<16>(L.a[q] + (uint32_t)C::KSTEP * s, stage + C::OFF_A + 1024 * chunk_of<typename C::DA, W>(q, wave));
     }
     if (L.mask & 4u) {
 #pragma unroll
         for (int q = 0; q < C::DB::per; q++)
-            dma<16>(L.b[q] + 64u * s, stage + C::OFF_B + 1024 * chunk_of<typename C::DB, W>(q, wave));
+            dma<16>(L.b[q] + (uint32_t)(C::KSTEP / 2) * s, stage + C::OFF_B + 1024 * chunk_of<typename C::DB, W>(q, wave));
     }
     if (L.mask & 2u) {
 #pragma unroll
         for (int q = 0; q < C::DSA::per; q++)
-            dma<4>(L.sa[q] + 4u * s, stage + C::OFF_SA + 256 * chunk_of<typename C::DSA, W>(q, wave));
+            dma<4>(L.sa[q] + 4u * C::KS * s, stage + C::OFF_SA + 256 * chunk_of<typename C::DSA, W>(q, wave));
     }
     if (L.mask & 1u) {
 #pragma unroll
         for (int q = 0; q < C::DSB::per; q++)
-            dma<4>(L.sb[q] + 4u * s, stage + C::OFF_SB + 256 * chunk_of<typename C::DSB, W>(q, wave));
+            dma<4>(L.sb[q] + 4u * C::KS * s, stage + C::OFF_SB + 256 * chunk_of<typename C::DSB, W>(q, wave));
     }
 }
 
@@ -341,9 +347,9 @@ __device__ __forceinline__ void wait_lgkm() {
  * soon as its reads have landed (lgkmcnt(count of the second half's
  * reads)), so the second half's LDS reads run under them.
  */
-template <class C>
-__device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
-                                          uint32_t wm, uint32_t wn) {
+template <class C, int KSI>
+__device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
+                                           uint32_t wm, uint32_t wn) {
     constexpr int NA = C::TERMS * C::WM, H1 = (NA + 1) / 2, H2 = NA - H1;
     static_assert(3 * H2 < 16, "second-half reads fit the lgkm counter");
     const uint32_t lane = threadIdx.x & 63u;
@@ -351,15 +357,19 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     const uint32_t base = lds_addr(st);
     const uint32_t a_lo = base + a_slot(c, g) + 2048u * C::WM * wm;
     const uint32_t a_hi = base + a_slot(c, 4u + g) + 2048u * C::WM * wm;
-    /* region bases in the address registers keep the immediates 16-bit */
-    const uint32_t b_base = base + C::OFF_B + 16u * lane + 1024u * C::WN * wn;
-    const uint32_t sa_base = base + C::OFF_SA + 4u * c + 64u * C::WM * wm;
-    const uint32_t sb_base = base + C::OFF_SB + 4u * c + 64u * C::WN * wn;
+    /* region bases in the address registers keep the immediates 16-bit;
+     * slice KSI's A chunks, scales and (KS = 2) B pieces 4 KSI + g */
+    const uint32_t b_base = C::KS == 2
+        ? base + C::OFF_B + a_slot(c, 4u * KSI + g) + 2048u * C::WN * wn
+        : base + C::OFF_B + 16u * lane + 1024u * C::WN * wn;
+    const uint32_t sa_base =
+        base + C::OFF_SA + 4u * (KSI * C::TERMS * C::SA_ROWS) + 4u * c + 64u * C::WM * wm;
+    const uint32_t sb_base = base + C::OFF_SB + 4u * (KSI * C::BN) + 4u * c + 64u * C::WN * wn;
     u32x4_t alo[NA], ahi[NA], bv[C::WN];
     uint32_t saw[NA], sbw[C::WN];
     auto read_a = [&](auto I) {
         constexpr int q = decltype(I)::value, t = q / C::WM, i = q % C::WM;
-        constexpr int off = C::OFF_A + 2048 * (t * (C::BM / 16) + i);
+        constexpr int off = C::OFF_A + 2048 * ((KSI * C::TERMS + t) * (C::BM / 16) + i);
         alo[q] = ds_read16<off>(a_lo);
         ahi[q] = ds_read16<off>(a_hi);
         saw[q] = ds_read4<4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
@@ -379,7 +389,7 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     };
     static_for<C::WN>([&](auto J) {
         constexpr int j = decltype(J)::value;
-        bv[j] = ds_read16<1024 * j>(b_base);
+        bv[j] = ds_read16<(C::KS == 2 ? 2048 : 1024) * j>(b_base);
         sbw[j] = ds_read4<64 * j>(sb_base);
     });
     if constexpr (C::SEQ) {
@@ -434,6 +444,17 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
     static_for<H2>([&](auto I) { mfmas(std::integral_constant<int, H1 + decltype(I)::value>{}); });
 }
 
+/* One staged step: its K slices in order. */
+template <class C>
+__device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
+                                          uint32_t wm, uint32_t wn) {
+    mfma_slice<C, 0>(acc, st, wm, wn);
+    if constexpr (C::KS == 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_slice<C, 1>(acc, st, wm, wn);
+    }
+}
+
 /* Step s of the ring: wait for this wave's loads of step s (one later step
  * may stay in flight), barrier (every wave's loads of s have landed and
  * every wave is done reading the buffer refilled next), refill `nxt` with
@@ -461,7 +482,7 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
                                               uint32_t wm, uint32_t wn) {
     static_assert(C::STAGES == 2 || C::STAGES == 3, "two or three buffers");
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t nsteps = K / 128u;
+    const uint32_t nsteps = K / (uint32_t)C::KSTEP;
     if constexpr (C::STAGES == 2) {
         /* Two buffers, for tiles whose stage is too big for three: the
          * step is long (one wave per SIMD, WM x WN x TERMS MFMAs each), so
@@ -597,25 +618,33 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
 #pragma unroll
         for (int q = 0; q < C::DA::per; q++) {
             const int ch = min(chunk_of<typename C::DA, W>(q, wave), C::A_CH - 1);
-            const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
-            L.a[q] = a_row(t, 16u * i + a_dma_row(lane, h)) + 16u * a_dma_piece(lane, h);
+            const int h = ch & 1, i = (ch >> 1) % (C::BM / 16);
+            const int t = (ch >> 1) / (C::BM / 16) % C::TERMS, ks = (ch >> 1) / (C::BM / 16) / C::TERMS;
+            L.a[q] = a_row(t, 16u * i + a_dma_row(lane, h)) + 128u * ks + 16u * a_dma_piece(lane, h);
         }
 #pragma unroll
         for (int q = 0; q < C::DB::per; q++) {
-            const int J = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
-            L.b[q] = wr_codes(J, c) + 16u * g;
+            const int ch = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
+            if constexpr (C::KS == 2) {
+                const uint32_t h = (uint32_t)ch & 1u;
+                L.b[q] = wr_codes(ch >> 1, a_dma_row(lane, h)) + 16u * a_dma_piece(lane, h);
+            } else {
+                L.b[q] = wr_codes(ch, c) + 16u * g;
+            }
         }
 #pragma unroll
         for (int q = 0; q < C::DSB::per; q++) {
             const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
-            L.sb[q] = wr_scl(ch * 4 + (int)g, c); /* 64 rows = 4 subtiles per chunk */
+            const int b = ch % (C::BN / 64), ks = ch / (C::BN / 64);
+            L.sb[q] = wr_scl(b * 4 + (int)g, c) + 4u * ks; /* 64 rows = 4 subtiles per chunk */
         }
 #pragma unroll
         for (int q = 0; q < C::DSA::per; q++) {
             const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
-            const int t = ch / (C::SA_ROWS / 64);
-            const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
-            L.sa[q] = a_scl(t, r);
+            const int tc = ch % (C::TERMS * C::SA_ROWS / 64), ks = ch / (C::TERMS * C::SA_ROWS / 64);
+            const int t = tc / (C::SA_ROWS / 64);
+            const uint32_t r = (uint32_t)((tc % (C::SA_ROWS / 64)) * 64) + lane;
+            L.sa[q] = a_scl(t, r) + 4u * ks;
         }
     }
     f32x4 acc[C::WM][C::WN];
@@ -700,25 +729,35 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
 #pragma unroll
     for (int q = 0; q < C::DA::per; q++) {
         const int ch = min(chunk_of<typename C::DA, W>(q, wave), C::A_CH - 1);
-        const int h = ch & 1, i = (ch >> 1) % (C::BM / 16), t = (ch >> 1) / (C::BM / 16);
-        L.a[q] = A.B.aq[t] + prow(16u * i + a_dma_row(lane, h)) * F + 16u * a_dma_piece(lane, h);
+        const int h = ch & 1, i = (ch >> 1) % (C::BM / 16);
+        const int t = (ch >> 1) / (C::BM / 16) % C::TERMS, ks = (ch >> 1) / (C::BM / 16) / C::TERMS;
+        L.a[q] = A.B.aq[t] + prow(16u * i + a_dma_row(lane, h)) * F + 128u * ks +
+                 16u * a_dma_piece(lane, h);
     }
 #pragma unroll
     for (int q = 0; q < C::DB::per; q++) {
-        const int J = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
-        L.b[q] = wp + (uint64_t)(d0 + 16u * J + c) * (F / 2u) + 16u * g;
+        const int ch = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
+        if constexpr (C::KS == 2) {
+            const uint32_t h = (uint32_t)ch & 1u;
+            L.b[q] = wp + (uint64_t)(d0 + 16u * (uint32_t)(ch >> 1) + a_dma_row(lane, h)) * (F / 2u) +
+                     16u * a_dma_piece(lane, h);
+        } else {
+            L.b[q] = wp + (uint64_t)(d0 + 16u * ch + c) * (F / 2u) + 16u * g;
+        }
     }
 #pragma unroll
     for (int q = 0; q < C::DSB::per; q++) {
         const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
-        L.sb[q] = ws + (uint64_t)(d0 + 64u * ch + lane) * (F / 32u);
+        const int b = ch % (C::BN / 64), ks = ch / (C::BN / 64);
+        L.sb[q] = ws + (uint64_t)(d0 + 64u * b + lane) * (F / 32u) + 4u * ks;
     }
 #pragma unroll
     for (int q = 0; q < C::DSA::per; q++) {
         const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
-        const int t = ch / (C::SA_ROWS / 64);
-        const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
-        L.sa[q] = A.B.as[t] + prow(r) * (F / 32u);
+        const int tc = ch % (C::TERMS * C::SA_ROWS / 64), ks = ch / (C::TERMS * C::SA_ROWS / 64);
+        const int t = tc / (C::SA_ROWS / 64);
+        const uint32_t r = (uint32_t)((tc % (C::SA_ROWS / 64)) * 64) + lane;
+        L.sa[q] = A.B.as[t] + prow(r) * (F / 32u) + 4u * ks;
     }
     f32x4 acc[C::WM][C::WN];
 #pragma unroll
@@ -743,9 +782,9 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
 /* Tile classes (rows per tile): 16, 64, 128. One-term class 0 computes
  * 32 rows so that its A chunks still split over four waves. */
 template <int TERMS>
-using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3>;
+using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2>;
 template <int TERMS>
-using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 3>;
+using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2>;
 /* 128 x 512 blocks: four waves, one per SIMD, each 64 activation rows x
  * 256 weight rows (accumulators in AGPRs); halves the activation re-reads
  * of a 256-wide block, two stage buffers */
