@@ -183,10 +183,11 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
     const float v = wave_sum_rows<2 * RPW>(p); /* lanes < 32: gate, lanes >= 32: up */
     const float u = __shfl_xor(v, 32, 64);
     const float gb = bf16_to_f32(f32_to_bf16(v)), ub = bf16_to_f32(f32_to_bf16(u));
-    const uint32_t bits = f32_to_bf16(gated_act(gb, ub, P.activation, P.beta, P.linear_beta));
-    /* lanes 0 and 32/RPW hold rows 2w and 2w+1 */
-    const uint32_t hi = (uint32_t)__shfl_down((int)bits, 32u / RPW, 64);
-    if (lane == 0u) *(uint32_t *)(dst + 2u * wave) = bits | (hi << 16);
+    const uint16_t bits = f32_to_bf16(gated_act(gb, ub, P.activation, P.beta, P.linear_beta));
+    /* gate row r of this wave sits on lanes 32 r / RPW .. (the up row r on
+     * the same lanes + 32) */
+    constexpr uint32_t kSpan = 32u / RPW;
+    if (lane < 32u && (lane & (kSpan - 1u)) == 0u) dst[RPW * wave + lane / kSpan] = bits;
 }
 
 /* ---------------------------------------------------------------------- */

@@ -121,6 +121,47 @@ def test_mxfp4_misaligned_8mod16(cuda):
     np.testing.assert_array_equal(host(out).view(np.uint16), want[0])
 
 
+def bf16_equal_or_both_nan(got, want):
+    """Bit equality, except that NaN outputs only need to be NaN on both
+    sides (the GPU's default NaN is positive, x86's negative)."""
+    got, want = np.asarray(got, np.uint16), np.asarray(want, np.uint16)
+    gnan = (got & 0x7FFF) > 0x7F80
+    wnan = (want & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal(gnan, wnan)
+    np.testing.assert_array_equal(got[~gnan], want[~gnan])
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_mxfp4_extreme_scales(cuda, T):
+    """E8M0 bytes 0 (2^-127, subnormal scale), 1, 254 and 255 (+inf, which the
+    reference's expert smoke test guards against in checkpoints) mixed into
+    ordinary scales: GEMV and batched GEMM match the oracle bit for bit,
+    including inf and inf*0 = NaN rows (k3_rocm_ops.cu:179-183)."""
+    rows, cols = 64, 512
+    rng = np.random.default_rng(11 + T)
+    p, s = rand_mx(rng, rows, cols)
+    special = np.array([0, 1, 254, 255], np.uint8)
+    mask = rng.random(s.shape) < 0.15
+    s[mask] = special[rng.integers(0, 4, mask.sum())]
+    s[0, :] = 0      # a row of only subnormal scales
+    s[1, :] = 254    # a row near overflow
+    p[2, :] = 0      # zero codes under an inf scale give NaN
+    s[2, 3] = 255
+    x = rand_bf16(rng, (T, cols))
+    out = torch.zeros((T, rows), dtype=torch.int16, device=cuda)
+    fn = ops.k3_rocm_mxfp4_gemv_bf16 if T == 1 else None
+    if T == 1:
+        assert fn(out, dev(p, cuda), dev(s, cuda), dev(x.view(np.int16), cuda), rows, cols)
+    else:
+        assert ops.k3_rocm_mxfp4_gemm_bf16(out, dev(p, cuda), dev(s, cuda),
+                                           dev(x.view(np.int16), cuda), T, rows, cols)
+    sync()
+    want, _ = O.mxfp4_gemm(p, s, x, rows, cols)
+    bf16_equal_or_both_nan(host(out).view(np.uint16), want)
+    got = host(out).view(np.uint16)
+    assert ((got[:, 2] & 0x7FFF) > 0x7F80).all(), "inf * 0 must give NaN"
+
+
 @pytest.mark.parametrize("T,E,H", [(1, 896, 7168), (3, 64, 2048), (17, 896, 7168), (4, 100, 1001),
                                    # blocked-GEMM path (T >= 128): ragged token/row tiles,
                                    # a partial last K step (65 chunks), XCD grouping with a
