@@ -31,7 +31,8 @@ extern "C" {
  * [rows, columns / 2] (low nibble = even column) and E8M0 scales
  * [rows, columns / 32]. Fields follow the six-tensor span order of
  * k3_prefill.c:71-75 (w1 = gate, w2 = down, w3 = up). Packed pointers must
- * be 16-byte aligned for the fused kernels.
+ * be 16-byte aligned for the fused kernels, and scale pointers too for the
+ * MXFP8 precisions (their kernels fetch scales 16 bytes per row at a time).
  */
 typedef struct {
     const void *gate_packed;  /* w1.weight_packed [ffn, hidden / 2]  */

@@ -190,11 +190,16 @@ struct TileCfg {
     static constexpr int KS = KS_, KSTEP = 128 * KS;
     static constexpr int BM = MW * 16 * WM, BN = NW * 16 * WN;
     static constexpr int A_CH = KS * TERMS * (BM / 16) * 2, B_CH = KS == 2 ? BN / 8 : BN / 16;
+    /* E8M0 scales live outside the stages, in two scale buffers: a scale
+     * block holds 16 bytes of every row (SQ stages' worth, 4 scales per 128
+     * K), so a row's scales arrive in one 16-byte request per SQ stages
+     * instead of a 4-byte request per stage. Chunk = 64 rows x 16 B. */
+    static constexpr int SQ = 4 / KS;
     static constexpr int SA_ROWS = BM < 64 ? 64 : BM;
-    static constexpr int SA_CH = KS * TERMS * SA_ROWS / 64, SB_CH = KS * BN / 64;
-    static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, OFF_SA = OFF_B + B_CH * 1024;
-    static constexpr int OFF_SB = OFF_SA + SA_CH * 256, STAGE = OFF_SB + SB_CH * 256;
-    static constexpr int LDS = STAGE * STAGES;
+    static constexpr int SA_CH = TERMS * SA_ROWS / 64, SB_CH = BN / 64;
+    static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, STAGE = OFF_B + B_CH * 1024;
+    static constexpr int OFF_SA = 0, OFF_SB = SA_CH * 1024, SBUF = (SA_CH + SB_CH) * 1024;
+    static constexpr int LDS = STAGE * STAGES + 2 * SBUF;
     /* two waves per SIMD (register-bound) read the second half of their A
      * fragments after the first half's MFMAs */
     static constexpr bool SEQ = NWV > 4;
@@ -205,9 +210,10 @@ struct TileCfg {
     using DSB = Deal<SB_CH, NWV>;
     /* loads per step of a wave holding the kinds flagged in `mask`
      * (bit 3 A, 2 B, 1 SA, 0 SB) */
+    /* (scale blocks are issued first in their stage's batch and are not
+     * counted: waiting on the count of A and B loads alone covers them) */
     static constexpr int loads(int mask) {
-        return ((mask & 8) ? DA::per : 0) + ((mask & 4) ? DB::per : 0) +
-               ((mask & 2) ? DSA::per : 0) + ((mask & 1) ? DSB::per : 0);
+        return ((mask & 8) ? DA::per : 0) + ((mask & 4) ? DB::per : 0);
     }
     static_assert(LDS <= 160 * 1024, "LDS");
     static_assert(loads(15) < 32, "vmcnt budget for one step in flight");
@@ -256,8 +262,22 @@ __device__ __forceinline__ uint32_t kinds_held(uint32_t wave) {
 
 template <class C>
 __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, uint32_t s,
-                                           uint32_t wave) {
+                                           uint32_t wave, uint8_t *sbuf0, uint8_t *sbuf1) {
     constexpr int W = C::NWV;
+    if (s % (uint32_t)C::SQ == 0u) { /* scale block s / SQ, before the stage's data */
+        const uint32_t b = s / (uint32_t)C::SQ;
+        uint8_t *sbuf = (b & 1u) ? sbuf1 : sbuf0;
+        if (L.mask & 2u) {
+#pragma unroll
+            for (int q = 0; q < C::DSA::per; q++)
+                dma<16>(L.sa[q] + 16u * b, sbuf + C::OFF_SA + 1024 * chunk_of<typename C::DSA, W>(q, wave));
+        }
+        if (L.mask & 1u) {
+#pragma unroll
+            for (int q = 0; q < C::DSB::per; q++)
+                dma<16>(L.sb[q] + 16u * b, sbuf + C::OFF_SB + 1024 * chunk_of<typename C::DSB, W>(q, wave));
+        }
+    }
     if (L.mask & 8u) {
 #pragma unroll
         for (int q = 0; q < C::DA::per; q++)
@@ -267,16 +287,6 @@ __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, u
 #pragma unroll
         for (int q = 0; q < C::DB::per; q++)
             dma<16>(L.b[q] + (uint32_t)(C::KSTEP / 2) * s, stage + C::OFF_B + 1024 * chunk_of<typename C::DB, W>(q, wave));
-    }
-    if (L.mask & 2u) {
-#pragma unroll
-        for (int q = 0; q < C::DSA::per; q++)
-            dma<4>(L.sa[q] + 4u * C::KS * s, stage + C::OFF_SA + 256 * chunk_of<typename C::DSA, W>(q, wave));
-    }
-    if (L.mask & 1u) {
-#pragma unroll
-        for (int q = 0; q < C::DSB::per; q++)
-            dma<4>(L.sb[q] + 4u * C::KS * s, stage + C::OFF_SB + 256 * chunk_of<typename C::DSB, W>(q, wave));
     }
 }
 
@@ -349,7 +359,8 @@ __device__ __forceinline__ void wait_lgkm() {
  */
 template <class C, int KSI>
 __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
-                                           uint32_t wm, uint32_t wn) {
+                                           const uint8_t *sbuf, uint32_t sq, uint32_t wm,
+                                           uint32_t wn) {
     constexpr int NA = C::TERMS * C::WM, H1 = (NA + 1) / 2, H2 = NA - H1;
     static_assert(3 * H2 < 16, "second-half reads fit the lgkm counter");
     const uint32_t lane = threadIdx.x & 63u;
@@ -362,9 +373,10 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
     const uint32_t b_base = C::KS == 2
         ? base + C::OFF_B + a_slot(c, 4u * KSI + g) + 2048u * C::WN * wn
         : base + C::OFF_B + 16u * lane + 1024u * C::WN * wn;
-    const uint32_t sa_base =
-        base + C::OFF_SA + 4u * (KSI * C::TERMS * C::SA_ROWS) + 4u * c + 64u * C::WM * wm;
-    const uint32_t sb_base = base + C::OFF_SB + 4u * (KSI * C::BN) + 4u * c + 64u * C::WN * wn;
+    /* scales: row r's dword for this K slice at 16 r + 4 (KS sq + KSI) */
+    const uint32_t sbase = lds_addr(sbuf) + 16u * c + 4u * (C::KS * sq + KSI);
+    const uint32_t sa_base = sbase + C::OFF_SA + 256u * C::WM * wm;
+    const uint32_t sb_base = sbase + C::OFF_SB + 256u * C::WN * wn;
     u32x4_t alo[NA], ahi[NA], bv[C::WN];
     uint32_t saw[NA], sbw[C::WN];
     auto read_a = [&](auto I) {
@@ -372,7 +384,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         constexpr int off = C::OFF_A + 2048 * ((KSI * C::TERMS + t) * (C::BM / 16) + i);
         alo[q] = ds_read16<off>(a_lo);
         ahi[q] = ds_read16<off>(a_hi);
-        saw[q] = ds_read4<4 * (t * C::SA_ROWS + 16 * i)>(sa_base);
+        saw[q] = ds_read4<16 * (t * C::SA_ROWS + 16 * i)>(sa_base);
     };
     auto mfmas = [&](auto Q) {
         constexpr int q = decltype(Q)::value, i = q % C::WM;
@@ -390,7 +402,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
     static_for<C::WN>([&](auto J) {
         constexpr int j = decltype(J)::value;
         bv[j] = ds_read16<(C::KS == 2 ? 2048 : 1024) * j>(b_base);
-        sbw[j] = ds_read4<64 * j>(sb_base);
+        sbw[j] = ds_read4<256 * j>(sb_base);
     });
     if constexpr (C::SEQ) {
         /* register-bound tiles: the second half's fragments are read into
@@ -447,11 +459,14 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
 /* One staged step: its K slices in order. */
 template <class C>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
+                                          const uint8_t *sbuf0, const uint8_t *sbuf1, uint32_t s,
                                           uint32_t wm, uint32_t wn) {
-    mfma_slice<C, 0>(acc, st, wm, wn);
+    const uint32_t b = s / (uint32_t)C::SQ, sq = s % (uint32_t)C::SQ;
+    const uint8_t *sbuf = (b & 1u) ? sbuf1 : sbuf0;
+    mfma_slice<C, 0>(acc, st, sbuf, sq, wm, wn);
     if constexpr (C::KS == 2) {
         __builtin_amdgcn_sched_barrier(0);
-        mfma_slice<C, 1>(acc, st, wm, wn);
+        mfma_slice<C, 1>(acc, st, sbuf, sq, wm, wn);
     }
 }
 
@@ -462,11 +477,12 @@ __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint
 template <class C>
 __device__ __forceinline__ void ring_step(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
                                           const uint8_t *cur, uint8_t *nxt, uint32_t s,
-                                          uint32_t nsteps, uint32_t wm, uint32_t wn) {
+                                          uint32_t nsteps, uint32_t wm, uint32_t wn,
+                                          uint8_t *sbuf0, uint8_t *sbuf1) {
     wait_step<C>(L, s + 1u < nsteps ? 1 : 0);
     __builtin_amdgcn_s_barrier();
-    if (s + 2u < nsteps) issue_step<C>(L, nxt, s + 2u, threadIdx.x >> 6);
-    mfma_step<C>(acc, cur, wm, wn);
+    if (s + 2u < nsteps) issue_step<C>(L, nxt, s + 2u, threadIdx.x >> 6, sbuf0, sbuf1);
+    mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn);
 }
 
 /*
@@ -478,8 +494,9 @@ __device__ __forceinline__ void ring_step(f32x4 (&acc)[C::WM][C::WN], const Load
  */
 template <class C>
 __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
-                                              uint8_t *b0, uint8_t *b1, uint8_t *b2, uint32_t K,
-                                              uint32_t wm, uint32_t wn) {
+                                              uint8_t *b0, uint8_t *b1, uint8_t *b2, uint8_t *sbuf0,
+                                              uint8_t *sbuf1, uint32_t K, uint32_t wm,
+                                              uint32_t wn) {
     static_assert(C::STAGES == 2 || C::STAGES == 3, "two or three buffers");
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nsteps = K / (uint32_t)C::KSTEP;
@@ -490,22 +507,22 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
         auto step2 = [&](uint32_t s, const uint8_t *cur, uint8_t *nxt) __attribute__((always_inline)) {
             wait_vm<0>();
             __builtin_amdgcn_s_barrier();
-            if (s + 1u < nsteps) issue_step<C>(L, nxt, s + 1u, wave);
-            mfma_step<C>(acc, cur, wm, wn);
+            if (s + 1u < nsteps) issue_step<C>(L, nxt, s + 1u, wave, sbuf0, sbuf1);
+            mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn);
         };
-        issue_step<C>(L, b0, 0u, wave);
+        issue_step<C>(L, b0, 0u, wave, sbuf0, sbuf1);
         for (uint32_t s = 0; s < nsteps; s += 2u) {
             step2(s, b0, b1);
             if (s + 1u < nsteps) step2(s + 1u, b1, b0);
         }
         return;
     }
-    issue_step<C>(L, b0, 0u, wave);
-    if (nsteps > 1u) issue_step<C>(L, b1, 1u, wave);
+    issue_step<C>(L, b0, 0u, wave, sbuf0, sbuf1);
+    if (nsteps > 1u) issue_step<C>(L, b1, 1u, wave, sbuf0, sbuf1);
     for (uint32_t s = 0; s < nsteps; s += 3u) {
-        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn);
-        if (s + 1u < nsteps) ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn);
-        if (s + 2u < nsteps) ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn);
+        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn, sbuf0, sbuf1);
+        if (s + 1u < nsteps) ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn, sbuf0, sbuf1);
+        if (s + 2u < nsteps) ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn, sbuf0, sbuf1);
     }
 }
 
@@ -573,6 +590,7 @@ struct GateUpArgs {
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sbuf0[C::SBUF], sbuf1[C::SBUF];
     __shared__ __attribute__((aligned(16))) uint8_t b2[C::STAGES == 3 ? C::STAGE : 16];
     uint32_t tile, colb;
     if (!xcd_work(*A.tile_count, A.F / (uint32_t)(C::BN / 2), tile, colb)) return;
@@ -633,18 +651,16 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
             }
         }
 #pragma unroll
-        for (int q = 0; q < C::DSB::per; q++) {
+        for (int q = 0; q < C::DSB::per; q++) { /* 64 rows = 4 subtiles per chunk */
             const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
-            const int b = ch % (C::BN / 64), ks = ch / (C::BN / 64);
-            L.sb[q] = wr_scl(b * 4 + (int)g, c) + 4u * ks; /* 64 rows = 4 subtiles per chunk */
+            L.sb[q] = wr_scl(ch * 4 + (int)g, c);
         }
 #pragma unroll
         for (int q = 0; q < C::DSA::per; q++) {
             const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
-            const int tc = ch % (C::TERMS * C::SA_ROWS / 64), ks = ch / (C::TERMS * C::SA_ROWS / 64);
-            const int t = tc / (C::SA_ROWS / 64);
-            const uint32_t r = (uint32_t)((tc % (C::SA_ROWS / 64)) * 64) + lane;
-            L.sa[q] = a_scl(t, r) + 4u * ks;
+            const int t = ch / (C::SA_ROWS / 64);
+            const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
+            L.sa[q] = a_scl(t, r);
         }
     }
     f32x4 acc[C::WM][C::WN];
@@ -652,7 +668,7 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_pipeline<C>(acc, L, b0, b1, b2, H, wm, wn);
+    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, H, wm, wn);
 
     const uint32_t fw0 = f0 + (uint32_t)FW * wn;
 #pragma unroll
@@ -710,6 +726,7 @@ struct DownArgs {
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t sbuf0[C::SBUF], sbuf1[C::SBUF];
     __shared__ __attribute__((aligned(16))) uint8_t b2[C::STAGES == 3 ? C::STAGE : 16];
     uint32_t tile, colb;
     if (!xcd_work(*A.tile_count, A.H / (uint32_t)C::BN, tile, colb)) return;
@@ -748,23 +765,21 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
 #pragma unroll
     for (int q = 0; q < C::DSB::per; q++) {
         const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
-        const int b = ch % (C::BN / 64), ks = ch / (C::BN / 64);
-        L.sb[q] = ws + (uint64_t)(d0 + 64u * b + lane) * (F / 32u) + 4u * ks;
+        L.sb[q] = ws + (uint64_t)(d0 + 64u * ch + lane) * (F / 32u);
     }
 #pragma unroll
     for (int q = 0; q < C::DSA::per; q++) {
         const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
-        const int tc = ch % (C::TERMS * C::SA_ROWS / 64), ks = ch / (C::TERMS * C::SA_ROWS / 64);
-        const int t = tc / (C::SA_ROWS / 64);
-        const uint32_t r = (uint32_t)((tc % (C::SA_ROWS / 64)) * 64) + lane;
-        L.sa[q] = A.B.as[t] + prow(r) * (F / 32u) + 4u * ks;
+        const int t = ch / (C::SA_ROWS / 64);
+        const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
+        L.sa[q] = A.B.as[t] + prow(r) * (F / 32u);
     }
     f32x4 acc[C::WM][C::WN];
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_pipeline<C>(acc, L, b0, b1, b2, F, wm, wn);
+    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, F, wm, wn);
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
