@@ -1,11 +1,13 @@
 /*
  * Single-token decode of the routed-MoE layer on gfx950: five kernels.
  *
- *   router_kernel   4 expert rows per block (one wave each): logit,
- *                   sigmoid score and order key per expert.
+ *   router_kernel   2 expert rows per one-wave block (the hidden state is
+ *                   read once for both): logit, sigmoid score and order
+ *                   key per expert.
  *   topk_kernel     one wave selects the routes (k3_topk.h) and resolves
- *                   the k selected expert descriptors once, so the expert
- *                   kernels reach their weights through a single load.
+ *                   the k selected expert descriptors once (their loads
+ *                   start before ranking), so the expert kernels reach
+ *                   their weights through a single load.
  *   gateup_kernel   one block per (slot, 8 F-rows): each of its four waves
  *                   streams one 64-group K-stripe of the 8 gate and 8 up
  *                   rows (a coalesced 1 KB row-stripe per load), group sums
@@ -14,7 +16,8 @@
  *                   flight.
  *   down_kernel     one block per (slot, 4 x 16 rows): each wave streams a
  *                   contiguous 16-row stripe of the slot's down matrix
- *                   (16 KB in flight per wave) and writes bf16 y[slot].
+ *                   (16 KB in flight per wave) against the activation
+ *                   staged once per block in LDS, and writes bf16 y[slot].
  *   combine_kernel  rank-order weighted sum of the k slot rows plus the
  *                   residual.
  *
@@ -46,47 +49,57 @@ constexpr int kDownRows = 16;         /* rows per down wave (F <= 2048) */
 /* router                                                                  */
 /* ---------------------------------------------------------------------- */
 
-/* Rows 4b..4b+3, w64 order (elements in chunks of 8; lane l owns chunks
- * l, l+64, ...; fmaf in column order; wave64 butterfly). Each wave loads
- * its weight row and the hidden state (cache hits after the first wave)
- * in one batch, so the whole row costs a single memory round trip. */
-__global__ __launch_bounds__(256) void router_kernel(DecodeParams P) {
-    const uint32_t lane = threadIdx.x & 63u;
+/* One wave per block computes rows 2b and 2b+1 in the w64 order (elements
+ * in chunks of 8; lane l owns chunks l, l+64, ...; fmaf in column order;
+ * wave64 butterfly). Both weight rows and the hidden state are loaded in
+ * one batch (one memory round trip), and the hidden state is read once
+ * for the two rows: a CU's L2 read bandwidth, not HBM, bounds this kernel,
+ * so rereading x per row would cost as much as a third of the weights. */
+__global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
+    const uint32_t lane = threadIdx.x;
     const uint32_t chunks = P.hidden / 8u;
-    const uint32_t row = 4u * blockIdx.x + (threadIdx.x >> 6);
-    if (row >= P.expert_count) return;
-    const uint4 *w4 = (const uint4 *)(P.router_weight + (uint64_t)row * P.hidden);
+    const uint32_t row0 = 2u * blockIdx.x;
+    const bool two = row0 + 1u < P.expert_count;
+    const uint4 *w0 = (const uint4 *)(P.router_weight + (uint64_t)row0 * P.hidden);
+    const uint4 *w1 = two ? w0 + chunks : w0;
     const uint4 *x4 = (const uint4 *)P.hidden_in;
-    uint4 wv[kRouterMaxChunks], xv[kRouterMaxChunks];
+    uint4 wa[kRouterMaxChunks], wb[kRouterMaxChunks], xv[kRouterMaxChunks];
 #pragma unroll
     for (int j = 0; j < kRouterMaxChunks; j++) {
         /* out-of-range chunks load chunk 0 and are skipped below */
         const uint32_t c = lane + 64u * j < chunks ? lane + 64u * j : 0u;
-        wv[j] = w4[c];
+        wa[j] = w0[c];
+        wb[j] = w1[c];
         xv[j] = x4[c];
     }
-    float a = 0.0f;
+    float a = 0.0f, b = 0.0f;
 #pragma unroll
     for (int j = 0; j < kRouterMaxChunks; j++) {
         if (lane + 64u * j < chunks) {
-            a = fmaf(bf16_lo(wv[j].x), bf16_lo(xv[j].x), a); a = fmaf(bf16_hi(wv[j].x), bf16_hi(xv[j].x), a);
-            a = fmaf(bf16_lo(wv[j].y), bf16_lo(xv[j].y), a); a = fmaf(bf16_hi(wv[j].y), bf16_hi(xv[j].y), a);
-            a = fmaf(bf16_lo(wv[j].z), bf16_lo(xv[j].z), a); a = fmaf(bf16_hi(wv[j].z), bf16_hi(xv[j].z), a);
-            a = fmaf(bf16_lo(wv[j].w), bf16_lo(xv[j].w), a); a = fmaf(bf16_hi(wv[j].w), bf16_hi(xv[j].w), a);
+            const float x8[8] = {bf16_lo(xv[j].x), bf16_hi(xv[j].x), bf16_lo(xv[j].y),
+                                 bf16_hi(xv[j].y), bf16_lo(xv[j].z), bf16_hi(xv[j].z),
+                                 bf16_lo(xv[j].w), bf16_hi(xv[j].w)};
+            const uint32_t pa[4] = {wa[j].x, wa[j].y, wa[j].z, wa[j].w};
+            const uint32_t pb[4] = {wb[j].x, wb[j].y, wb[j].z, wb[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                a = fmaf(bf16_lo(pa[q]), x8[2 * q], a);
+                a = fmaf(bf16_hi(pa[q]), x8[2 * q + 1], a);
+                b = fmaf(bf16_lo(pb[q]), x8[2 * q], b);
+                b = fmaf(bf16_hi(pb[q]), x8[2 * q + 1], b);
+            }
         }
     }
-    const float v = wave_sum(a);
-    if (lane == 0u) {
+    const float va = wave_sum(a), vb = wave_sum(b);
+    if (lane < (two ? 2u : 1u)) {
+        const uint32_t row = row0 + lane;
+        const float v = lane ? vb : va;
         const float score = det_sigmoid(v);
         P.logits[row] = v;
         P.scores[row] = score;
         P.keys[row] = choice_key(score, P.router_bias[row]);
     }
 }
-
-/* ---------------------------------------------------------------------- */
-/* top-k + expert descriptors                                              */
-/* ---------------------------------------------------------------------- */
 
 /* Lane s < top_k stores the descriptor of route s (id `e`) and the wave
  * publishes the mask of slots that have an expert. One wave. */
@@ -99,11 +112,27 @@ __device__ __forceinline__ void resolve_slot(const DecodeParams &P, uint32_t e) 
     if (s == 0u) *P.slot_mask = (uint32_t)live;
 }
 
-/* One wave: select, then resolve the selected descriptors straight from
- * the ids the selection leaves in registers. */
+/* Descriptor hand-off of the decode top-k: each candidate lane starts the
+ * load of its expert's descriptor before ranking, and the lane whose
+ * candidate takes rank r stores it to slot r. */
+struct ResolveHooks {
+    const DecodeParams &P;
+    uint32_t *live_bits; /* LDS: bit r = slot r has an expert */
+    k3_moe_expert d{};
+    __device__ __forceinline__ void candidate(uint32_t id) { d = P.experts[id]; }
+    __device__ __forceinline__ void selected(uint32_t rank) {
+        P.sel[rank] = d;
+        if (d.down_packed) atomicOr(live_bits, 1u << rank);
+    }
+};
+
+/* One wave: select and resolve; slots past the selected routes get empty
+ * descriptors. */
 __global__ __launch_bounds__(64) void topk_kernel(DecodeParams P) {
     __shared__ TopkWaveSmem sm;
+    __shared__ uint32_t live_bits;
     const uint32_t lane = threadIdx.x;
+    if (lane == 0u) live_bits = 0u;
     uint32_t key[kTopkSlots];
     float score[kTopkSlots];
 #pragma unroll
@@ -113,8 +142,11 @@ __global__ __launch_bounds__(64) void topk_kernel(DecodeParams P) {
         score[j] = e < P.expert_count ? P.scores[e] : 0.0f;
     }
     const uint32_t id = topk_select_wave(key, score, P.top_k, P.scale, P.ids, P.weights,
-                                         P.ids_copy, P.weights_copy, sm);
-    resolve_slot(P, id);
+                                         P.ids_copy, P.weights_copy, sm,
+                                         ResolveHooks{P, &live_bits});
+    if (lane < P.top_k && id == UINT32_MAX) P.sel[lane] = k3_moe_expert{};
+    wave_fence();
+    if (lane == 0u) *P.slot_mask = live_bits;
 }
 
 /* descriptors for routes given by the caller */
@@ -199,7 +231,12 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
  * stream keeps many small blocks in flight: grid (H / (4 RB), k), block
  * 256; wave w of block (b, slot) computes rows (4b + w) RB .. + RB of slot
  * `slot` -- a contiguous RB-row stripe of its down matrix, all loads issued
- * at once. Lane l owns groups l, l + 64, ... (M of them: F <= 2048 M); per
+ * at once. The block stages the slot's activation in LDS once and each
+ * wave its RB x F/32 scale bytes (one contiguous run) with dword loads:
+ * the per-CU L2 request rate, not HBM, bounds this kernel, and per-wave
+ * activation reads and per-row byte loads of the scales added a third
+ * to the weight stream's requests. Lane l owns groups l, l + 64, ... (M
+ * of them: F <= 2048 M); per
  * row the group sum runs over the 32 columns in order, with 8-column
  * chunks of the activation converted once for the RB rows. Output y[slot,
  * d] = bf16(row sum), the reference's per-slot GEMV result
@@ -207,35 +244,78 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
  */
 template <int M, int RB>
 __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    static_assert(RB * 64 * M == 1024, "a wave's scale block is at most 1 KB");
+    /* the slot's activation, chunk (g, q) (8 columns, 32 g + 8 q) at
+     * q * 64 M + g, so lane-consecutive reads are bank-consecutive */
+    __shared__ uint4 xs[4 * 64 * M];
+    __shared__ uint32_t ssc[4][256]; /* each wave's RB x G scale bytes */
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, t = threadIdx.x;
     const uint32_t slot = blockIdx.y;
     const uint32_t row0 = (4u * blockIdx.x + wave) * RB;
     const uint32_t F = P.ffn, G = F / 32u;
     uint16_t *y = P.y + (uint64_t)slot * P.hidden + row0;
     const k3_moe_expert ex = P.sel[slot];
-    if (!ex.down_packed) {
+    if (!ex.down_packed) { /* uniform over the block */
         if (lane < (uint32_t)RB) y[lane] = 0;
         return;
     }
-    float acc[RB];
-#pragma unroll
-    for (int i = 0; i < RB; i++) acc[i] = 0.0f;
     const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
     const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
     const uint4 *a4 = (const uint4 *)(P.act + (uint64_t)slot * F);
+    /* issue order: the first weight stripe, then the block's activation
+     * (one load per thread instead of one per wave) and the wave's scale
+     * bytes (RB G contiguous bytes, dword loads when aligned) */
+    uint4 w[RB];
+    if (lane < G) {
+#pragma unroll
+        for (int i = 0; i < RB; i++)
+            w[i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * lane));
+    }
+    uint4 xa[M];
+#pragma unroll
+    for (int k = 0; k < M; k++) {
+        const uint32_t c = t + 256u * k;
+        if (c < 4u * G) xa[k] = gload(a4 + c);
+    }
+    const uint32_t nbytes = RB * G;
+    uint32_t sw[4];
+    const bool words = ((uintptr_t)ds & 3u) == 0u;
+    if (words) {
+        const uint32_t *dw = (const uint32_t *)ds;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (4u * (lane + 64u * k) < nbytes) sw[k] = *(const __attribute__((address_space(1))) uint32_t *)(dw + lane + 64u * k);
+    }
+#pragma unroll
+    for (int k = 0; k < M; k++) {
+        const uint32_t c = t + 256u * k;
+        if (c < 4u * G) xs[(c & 3u) * 64u * M + (c >> 2)] = xa[k];
+    }
+    if (words) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (4u * (lane + 64u * k) < nbytes) ssc[wave][lane + 64u * k] = sw[k];
+    } else {
+        uint8_t *sb = (uint8_t *)ssc[wave];
+        for (uint32_t b = lane; b < nbytes; b += 64u) sb[b] = (uint8_t)gload(ds + b);
+    }
+    __syncthreads();
+    const uint8_t *sb = (const uint8_t *)ssc[wave];
+    float acc[RB];
+#pragma unroll
+    for (int i = 0; i < RB; i++) acc[i] = 0.0f;
 #pragma unroll
     for (int m = 0; m < M; m++) {
         const uint32_t g = lane + 64u * m;
         if (g < G) {
-            uint4 w[RB], xr[4];
-            uint32_t sc[RB];
+            if (m > 0) {
 #pragma unroll
-            for (int i = 0; i < RB; i++) {
-                w[i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g));
-                sc[i] = gload(ds + (uint64_t)i * G + g);
+                for (int i = 0; i < RB; i++)
+                    w[i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g));
             }
+            uint4 xr[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) xr[q] = gload(a4 + 4u * g + q);
+            for (int q = 0; q < 4; q++) xr[q] = xs[q * 64 * M + g];
             float gs[RB];
 #pragma unroll
             for (int i = 0; i < RB; i++) gs[i] = 0.0f;
@@ -251,7 +331,8 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
                 }
             }
 #pragma unroll
-            for (int i = 0; i < RB; i++) acc[i] = fmaf(gs[i], e8m0_to_f32(sc[i]), acc[i]);
+            for (int i = 0; i < RB; i++)
+                acc[i] = fmaf(gs[i], e8m0_to_f32(sb[(uint32_t)i * G + g]), acc[i]);
         }
     }
     const float v = wave_sum_rows<RB>(acc);
@@ -295,7 +376,7 @@ bool decode_supported(const k3_moe_shape &s) {
 
 bool decode_launch(const DecodeParams &P, hipStream_t st, const StageMarker &mark) {
     mark(K3_MOE_STAGE_ROUTER);
-    hipLaunchKernelGGL(router_kernel, dim3((P.expert_count + 3u) / 4u), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(router_kernel, dim3((P.expert_count + 1u) / 2u), dim3(64), 0, st, P);
     mark(K3_MOE_STAGE_TOPK);
     hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(64), 0, st, P);
     return decode_launch_experts(P, st, mark, false);

@@ -9,14 +9,17 @@
  * missing slots (fewer than top_k selectable experts) get id UINT32_MAX and
  * weight 0.
  *
- * Method: choices are mapped to order-preserving 32-bit keys (0 = not
- * selectable). The top_k-th largest per-lane maximum is a lower bound on
- * the top_k-th largest key, so only keys at or above it (a few dozen for
- * real router outputs) are ranked, by counting with early exit. This is
- * wave-synchronous (no block barrier) and free of LDS atomics; a radix
- * histogram serialised on atomics because one token's keys cluster in a
- * few high-order bins, and a bitwise ballot search paid a VALU-to-scalar
- * round trip per count.
+ * Method (one wave, no block barrier, no atomics): choices are mapped to
+ * order-preserving 32-bit keys (0 = not selectable). The top_k-th largest
+ * per-lane maximum M is a lower bound on the top_k-th largest key (the
+ * top_k lanes with the largest maxima hold top_k keys >= M), so only keys
+ * >= M are ranked -- a few dozen for real router outputs. M is found by a
+ * 32-step bitwise search over the lane maxima (one ballot per bit). The
+ * candidates are compacted to one per lane (positions from a ballot-based
+ * prefix sum of the per-lane counts) and ranked from registers with
+ * readlane broadcasts, so the only LDS round trips are the compaction and
+ * the hand-over of the selected routes to their rank lanes. More than 64
+ * candidates (heavy ties) are ranked in 64-candidate passes from LDS.
  *
  * Lane l holds experts e = l + 64 j, j < kTopkSlots (E <= 1024).
  */
@@ -29,7 +32,6 @@ namespace k3 {
 constexpr int kTopkSlots = 16;
 
 struct TopkWaveSmem {
-    uint32_t lmax[64];
     uint32_t cand_key[1024];
     uint32_t cand_id[1024];
     float cand_score[1024];
@@ -50,92 +52,136 @@ __device__ __forceinline__ void wave_fence() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
 }
 
+/* Per-candidate hooks of topk_select_wave; the default does nothing.
+ * candidate(id): called by each lane holding a candidate before ranking
+ * (e.g. to start loads keyed by the id); selected(rank): called by that
+ * lane when its candidate takes rank `rank` < top_k. */
+struct TopkNoHooks {
+    __device__ __forceinline__ void candidate(uint32_t) {}
+    __device__ __forceinline__ void selected(uint32_t) {}
+};
+
+/* Rank of candidate (mk, mi) among the candidates held one per lane
+ * (lanes without one hold key 0): the number ordered before it by (key
+ * desc, id asc). */
+__device__ __forceinline__ uint32_t topk_rank_lanes(uint32_t mk, uint32_t mi, uint32_t ncand) {
+    uint32_t cnt = 0u;
+    for (uint32_t i0 = 0; i0 < ncand; i0 += 8u) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++) {
+            const uint32_t ok = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)(i0 + i));
+            const uint32_t oi = (uint32_t)__builtin_amdgcn_readlane((int)mi, (int)(i0 + i));
+            cnt += (ok > mk || (ok == mk && oi < mi)) ? 1u : 0u;
+        }
+    }
+    return cnt;
+}
+
 /* key[j]/score[j] for expert lane + 64 j. Writes ids/weights[0..top_k) (and
  * the optional copies, which may be host-mapped). Must be called by all 64
- * lanes of the wave; top_k <= 32. With `publish`, ids/weights are written
- * with write-through agent-scope stores (for readers in the same kernel).
- * Returns the rank-`lane` id to lanes < top_k (UINT32_MAX elsewhere). */
+ * lanes of the wave; 1 <= top_k <= 32. Returns the rank-`lane` id to lanes
+ * < top_k (UINT32_MAX elsewhere). */
+template <class Hooks = TopkNoHooks>
 __device__ __forceinline__ uint32_t topk_select_wave(const uint32_t (&key)[kTopkSlots],
-                                                 const float (&score)[kTopkSlots],
-                                                 uint32_t top_k, float scale, uint32_t *ids,
-                                                 float *weights, uint32_t *ids_copy,
-                                                 float *w_copy, TopkWaveSmem &sm,
-                                                 bool publish = false) {
+                                                     const float (&score)[kTopkSlots],
+                                                     uint32_t top_k, float scale, uint32_t *ids,
+                                                     float *weights, uint32_t *ids_copy,
+                                                     float *w_copy, TopkWaveSmem &sm,
+                                                     Hooks &&hooks = Hooks{}) {
     const uint32_t lane = threadIdx.x & 63u;
     const unsigned long long below = (1ull << lane) - 1ull;
-    /* Threshold: the top_k-th largest lane maximum M. The top_k lanes with
-     * the largest maxima hold top_k keys >= M, so every key of the true
-     * top_k is >= M: only keys >= M need ranking. */
+    /* threshold: the largest M with at least top_k lane maxima >= M, i.e.
+     * the top_k-th largest lane maximum */
     uint32_t lmax = 0u;
 #pragma unroll
     for (int j = 0; j < kTopkSlots; j++) lmax = key[j] > lmax ? key[j] : lmax;
-    sm.lmax[lane] = lmax;
-    wave_fence();
-    uint32_t r = 0u;
+    uint32_t thr = 0u;
 #pragma unroll
-    for (uint32_t i = 0; i < 64u; i++) {
-        const uint32_t v = sm.lmax[i];
-        r += (v > lmax || (v == lmax && i < lane)) ? 1u : 0u;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t t = thr | (1u << b);
+        if ((uint32_t)__popcll(__ballot(lmax >= t)) >= top_k) thr = t;
     }
-    const unsigned long long pm = __ballot(r == top_k - 1u);
-    uint32_t thr = (uint32_t)__shfl((int)lmax, pm ? __ffsll((long long)pm) - 1 : 0, 64);
     if (thr == 0u) thr = 1u; /* key 0 = not selectable */
-    /* candidates in id order (j asc, lane asc) */
-    uint32_t ncand = 0u;
+    /* candidate positions: exclusive prefix sum of the per-lane counts */
+    uint32_t mine = 0u;
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) mine += key[j] >= thr ? 1u : 0u;
+    uint32_t pos = 0u, ncand = 0u;
+#pragma unroll
+    for (int b = 0; b < 5; b++) { /* mine <= 16 */
+        const unsigned long long m = __ballot((mine >> b) & 1u);
+        pos += (uint32_t)__popcll(m & below) << b;
+        ncand += (uint32_t)__popcll(m) << b;
+    }
 #pragma unroll
     for (int j = 0; j < kTopkSlots; j++) {
-        const bool take = key[j] >= thr;
-        const unsigned long long m = __ballot(take);
-        if (take) {
-            const uint32_t pos = ncand + (uint32_t)__popcll(m & below);
+        if (key[j] >= thr) {
             sm.cand_key[pos] = key[j];
             sm.cand_id[pos] = lane + 64u * j;
             sm.cand_score[pos] = score[j];
+            pos++;
         }
-        ncand += (uint32_t)__popcll(m);
     }
     wave_fence();
-    /* rank = number of candidates ordered before (key desc, id asc); a
-     * candidate stops counting once it cannot be selected */
-    for (uint32_t base = 0; base < ncand; base += 64u) {
-        const uint32_t c = base + lane;
-        const bool live = c < ncand;
-        const uint32_t mk = live ? sm.cand_key[c] : 0u, mi = live ? sm.cand_id[c] : 0u;
-        uint32_t cnt = live ? 0u : top_k;
-        for (uint32_t i0 = 0; i0 < ncand; i0 += 16u) {
-#pragma unroll
-            for (uint32_t i = i0; i < i0 + 16u; i++) {
-                const uint32_t ok = i < ncand ? sm.cand_key[i] : 0u;
-                const uint32_t oi = sm.cand_id[i < ncand ? i : 0u];
-                cnt += (i < ncand && (ok > mk || (ok == mk && oi < mi))) ? 1u : 0u;
-            }
-            if (__ballot(cnt < top_k) == 0ull) break;
-        }
-        if (cnt < top_k) {
+    if (ncand <= 64u) {
+        const bool live = lane < ncand;
+        const uint32_t mk = live ? sm.cand_key[lane] : 0u, mi = live ? sm.cand_id[lane] : 0u;
+        if (live) hooks.candidate(mi);
+        const uint32_t cnt = topk_rank_lanes(mk, mi, ncand);
+        if (live && cnt < top_k) {
             sm.out_id[cnt] = mi;
-            sm.out_score[cnt] = sm.cand_score[c];
+            sm.out_score[cnt] = sm.cand_score[lane];
+            hooks.selected(cnt);
+        }
+    } else {
+        /* rank = number of candidates ordered before (key desc, id asc); a
+         * candidate stops counting once it cannot be selected */
+        for (uint32_t base = 0; base < ncand; base += 64u) {
+            const uint32_t c = base + lane;
+            const bool live = c < ncand;
+            const uint32_t mk = live ? sm.cand_key[c] : 0u, mi = live ? sm.cand_id[c] : 0u;
+            if (live) hooks.candidate(mi);
+            uint32_t cnt = live ? 0u : top_k;
+            for (uint32_t i0 = 0; i0 < ncand; i0 += 16u) {
+#pragma unroll
+                for (uint32_t i = i0; i < i0 + 16u; i++) {
+                    const uint32_t ok = i < ncand ? sm.cand_key[i] : 0u;
+                    const uint32_t oi = sm.cand_id[i < ncand ? i : 0u];
+                    cnt += (i < ncand && (ok > mk || (ok == mk && oi < mi))) ? 1u : 0u;
+                }
+                if (__ballot(cnt < top_k) == 0ull) break;
+            }
+            if (cnt < top_k) {
+                sm.out_id[cnt] = mi;
+                sm.out_score[cnt] = sm.cand_score[c];
+                hooks.selected(cnt);
+            }
         }
     }
     wave_fence();
     const uint32_t nsel = ncand < top_k ? ncand : top_k;
     /* lane r holds the rank-r score; the denominator adds them in rank
-     * order (a sequential chain over lane reads) */
+     * order (1e-20 first). Ranks >= nsel hold +0, which leaves the sum
+     * unchanged, so the chain runs over a fixed 16 or 32 lanes. */
     const float my_score = lane < nsel ? sm.out_score[lane] : 0.0f;
+    float sv[32];
+#pragma unroll
+    for (int q = 0; q < 32; q++)
+        sv[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                              __builtin_bit_cast(int, my_score), q));
     float den = 1e-20f;
-    for (uint32_t q = 0; q < top_k; q++)
-        den = __fadd_rn(den, __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                 __builtin_bit_cast(int, my_score), (int)q)));
+#pragma unroll
+    for (int q = 0; q < 16; q++) den = __fadd_rn(den, sv[q]);
+    if (top_k > 16u) {
+#pragma unroll
+        for (int q = 16; q < 32; q++) den = __fadd_rn(den, sv[q]);
+    }
     uint32_t id = UINT32_MAX;
     if (lane < top_k) {
         id = lane < nsel ? sm.out_id[lane] : UINT32_MAX;
         const float wr = __fmul_rn(__fdiv_rn(my_score, den), scale);
-        if (publish) {
-            __hip_atomic_store(ids + lane, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(weights + lane, wr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            ids[lane] = id;
-            weights[lane] = wr;
-        }
+        ids[lane] = id;
+        weights[lane] = wr;
         if (ids_copy) ids_copy[lane] = id;
         if (w_copy) w_copy[lane] = wr;
     }
