@@ -14,9 +14,9 @@
  *                   meet in LDS and are combined in the w64 lane order, then
  *                   the activation. 4096 blocks keep ~64 MB of loads in
  *                   flight.
- *   down_kernel     one block per (slot, 4 x 16 rows): each wave streams a
- *                   contiguous 16-row stripe of the slot's down matrix
- *                   (16 KB in flight per wave) against the activation
+ *   down_kernel     one block per (slot, 4 x 8 rows): each wave streams a
+ *                   contiguous 8-row stripe of the slot's down matrix
+ *                   (8 KB in flight per wave) against the activation
  *                   staged once per block in LDS, and writes bf16 y[slot].
  *   combine_kernel  rank-order weighted sum of the k slot rows plus the
  *                   residual.
@@ -43,7 +43,10 @@ namespace {
 
 constexpr int kRouterMaxChunks = 16;  /* hidden <= 8192 */
 constexpr int kGU = 8;                /* gate (and up) rows per gate/up block */
-constexpr int kDownRows = 16;         /* rows per down wave (F <= 2048) */
+/* rows per down wave (F <= 2048): 8 gives 3584 blocks for the K3 shape,
+ * enough for an even tail (16 rows: 1.75 rounds of resident blocks, ~1.5
+ * us slower per layer; 4 rows: no better than 8) */
+constexpr int kDownRows = 8;
 
 /* ---------------------------------------------------------------------- */
 /* router                                                                  */
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
  */
 template <int M, int RB>
 __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
-    static_assert(RB * 64 * M == 1024, "a wave's scale block is at most 1 KB");
+    static_assert(RB * 64 * M <= 1024, "a wave's scale block is at most 1 KB");
     /* the slot's activation, chunk (g, q) (8 columns, 32 g + 8 q) at
      * q * 64 M + g, so lane-consecutive reads are bank-consecutive */
     __shared__ uint4 xs[4 * 64 * M];
