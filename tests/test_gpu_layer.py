@@ -13,7 +13,7 @@ import torch
 import _oracle as O
 from moonshine_amd import layer as L
 from moonshine_amd._lib import lib
-from moonshine_amd.synth import CONFIGS, K3_NATIVE, make_inputs
+from moonshine_amd.synth import CONFIGS, K3_NATIVE, Config, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -87,7 +87,14 @@ def test_synth_store_host_matches_device(cuda):
     assert s.min() >= 121 and s.max() <= 125
 
 
-@pytest.mark.parametrize("cfg", [CONFIGS[0], CONFIGS[1], K3_NATIVE], ids=lambda c: c.name)
+# decode shapes beyond the BASELINE configs: a hidden size that is not a
+# multiple of the larger kernels' row tiles (6208 = 97 x 64), and top_k > 16
+DECODE_RAGGED = Config("decode-ragged-rows", 1, 6208, 128, 8, 1024, seed=1006)
+DECODE_TOPK20 = Config("decode-topk20", 1, 2048, 128, 20, 512, seed=1007)
+
+
+@pytest.mark.parametrize("cfg", [CONFIGS[0], CONFIGS[1], K3_NATIVE, DECODE_RAGGED, DECODE_TOPK20],
+                         ids=lambda c: c.name)
 def test_decode_layer_bitexact(cuda, cfg):
     inputs = make_inputs(cfg)
     moe = get_layer(cfg, inputs, cuda)
