@@ -360,7 +360,7 @@ __device__ __forceinline__ void wait_lgkm() {
 template <class C, int KSI>
 __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
                                            const uint8_t *sbuf, uint32_t sq, uint32_t wm,
-                                           uint32_t wn) {
+                                           uint32_t wn, uint32_t live) {
     constexpr int NA = C::TERMS * C::WM, H1 = (NA + 1) / 2, H2 = NA - H1;
     static_assert(3 * H2 < 16, "second-half reads fit the lgkm counter");
     const uint32_t lane = threadIdx.x & 63u;
@@ -391,6 +391,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         const i32x8 af = i32x8{(int)alo[q].x, (int)alo[q].y, (int)alo[q].z, (int)alo[q].w,
                                (int)ahi[q].x, (int)ahi[q].y, (int)ahi[q].z, (int)ahi[q].w};
         const int sa = (int)((saw[q] >> (8u * g)) & 255u);
+        if ((uint32_t)i >= live) return; /* row block past the tile's rows */
         static_for<C::WN>([&](auto J) {
             constexpr int j = decltype(J)::value;
             const i32x8 bf = i32x8{(int)bv[j].x, (int)bv[j].y, (int)bv[j].z, (int)bv[j].w, 0, 0, 0, 0};
@@ -460,13 +461,13 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
 template <class C>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
                                           const uint8_t *sbuf0, const uint8_t *sbuf1, uint32_t s,
-                                          uint32_t wm, uint32_t wn) {
+                                          uint32_t wm, uint32_t wn, uint32_t live) {
     const uint32_t b = s / (uint32_t)C::SQ, sq = s % (uint32_t)C::SQ;
     const uint8_t *sbuf = (b & 1u) ? sbuf1 : sbuf0;
-    mfma_slice<C, 0>(acc, st, sbuf, sq, wm, wn);
+    mfma_slice<C, 0>(acc, st, sbuf, sq, wm, wn, live);
     if constexpr (C::KS == 2) {
         __builtin_amdgcn_sched_barrier(0);
-        mfma_slice<C, 1>(acc, st, sbuf, sq, wm, wn);
+        mfma_slice<C, 1>(acc, st, sbuf, sq, wm, wn, live);
     }
 }
 
@@ -478,11 +479,21 @@ template <class C>
 __device__ __forceinline__ void ring_step(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
                                           const uint8_t *cur, uint8_t *nxt, uint32_t s,
                                           uint32_t nsteps, uint32_t wm, uint32_t wn,
-                                          uint8_t *sbuf0, uint8_t *sbuf1) {
+                                          uint8_t *sbuf0, uint8_t *sbuf1, uint32_t live) {
     wait_step<C>(L, s + 1u < nsteps ? 1 : 0);
     __builtin_amdgcn_s_barrier();
     if (s + 2u < nsteps) issue_step<C>(L, nxt, s + 2u, threadIdx.x >> 6, sbuf0, sbuf1);
-    mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn);
+    mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn, live);
+}
+
+/* 16-row blocks of wave row wm that hold tile rows (< rows): MFMAs of
+ * the others are skipped (their fragments are still read, which keeps the
+ * LDS wait counts fixed). Wave-uniform. */
+template <class C>
+__device__ __forceinline__ uint32_t live_blocks(uint32_t rows, uint32_t wm) {
+    const uint32_t r0 = 16u * (uint32_t)C::WM * wm;
+    const uint32_t n = rows > r0 ? (rows - r0 + 15u) / 16u : 0u;
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(n < (uint32_t)C::WM ? n : (uint32_t)C::WM));
 }
 
 /*
@@ -496,7 +507,7 @@ template <class C>
 __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
                                               uint8_t *b0, uint8_t *b1, uint8_t *b2, uint8_t *sbuf0,
                                               uint8_t *sbuf1, uint32_t K, uint32_t wm,
-                                              uint32_t wn) {
+                                              uint32_t wn, uint32_t live) {
     static_assert(C::STAGES == 2 || C::STAGES == 3, "two or three buffers");
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nsteps = K / (uint32_t)C::KSTEP;
@@ -508,7 +519,7 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
             wait_vm<0>();
             __builtin_amdgcn_s_barrier();
             if (s + 1u < nsteps) issue_step<C>(L, nxt, s + 1u, wave, sbuf0, sbuf1);
-            mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn);
+            mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn, live);
         };
         issue_step<C>(L, b0, 0u, wave, sbuf0, sbuf1);
         for (uint32_t s = 0; s < nsteps; s += 2u) {
@@ -520,9 +531,9 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
     issue_step<C>(L, b0, 0u, wave, sbuf0, sbuf1);
     if (nsteps > 1u) issue_step<C>(L, b1, 1u, wave, sbuf0, sbuf1);
     for (uint32_t s = 0; s < nsteps; s += 3u) {
-        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn, sbuf0, sbuf1);
-        if (s + 1u < nsteps) ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn, sbuf0, sbuf1);
-        if (s + 2u < nsteps) ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn, sbuf0, sbuf1);
+        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn, sbuf0, sbuf1, live);
+        if (s + 1u < nsteps) ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn, sbuf0, sbuf1, live);
+        if (s + 2u < nsteps) ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn, sbuf0, sbuf1, live);
     }
 }
 
@@ -668,7 +679,7 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, H, wm, wn);
+    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, H, wm, wn, live_blocks<C>(rows, wm));
 
     const uint32_t fw0 = f0 + (uint32_t)FW * wn;
 #pragma unroll
@@ -779,7 +790,7 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, F, wm, wn);
+    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, F, wm, wn, live_blocks<C>(rows, wm));
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
