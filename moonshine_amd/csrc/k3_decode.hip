@@ -163,7 +163,7 @@ __global__ __launch_bounds__(64) void resolve_kernel(DecodeParams P) {
 
 struct GateUpSmem {
     float part[2 * kGU][4][64];
-    float scl[2 * kGU][4][64];
+    uint32_t scl[2 * kGU][64]; /* raw E8M0 bytes of row r, groups 0 .. G - 1 */
 };
 
 /* grid (F / kGU, k), block 256; H <= 8192 (four 64-group stripes). */
@@ -179,27 +179,56 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
         return;
     }
     const uint32_t g = 64u * wave + lane;
+    const uint8_t *gs = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G;
+    const uint8_t *us = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G;
+    /* the block's scales are two contiguous runs of kGU G bytes (gate,
+     * up): fetched as whole lines of dwords, thread-contiguous, instead of
+     * a byte load per row and wave */
+    const bool words = G % 4u == 0u && (((uintptr_t)gs | (uintptr_t)us) & 3u) == 0u;
+    const uint32_t t = threadIdx.x, nd = kGU * G / 4u; /* dwords per run */
+    uint4 w[2 * kGU];
+    uint32_t sw[4];
     if (g < G) {
         const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u) + 16u * g;
         const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u) + 16u * g;
-        const uint8_t *gs = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G + g;
-        const uint8_t *us = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G + g;
-        uint4 w[2 * kGU];
-        uint32_t sc[2 * kGU];
 #pragma unroll
         for (int i = 0; i < kGU; i++) {
             w[i] = gload((const uint4 *)(gp + (uint64_t)i * (H / 2u)));
             w[kGU + i] = gload((const uint4 *)(up + (uint64_t)i * (H / 2u)));
-            sc[i] = gload(gs + (uint64_t)i * G);
-            sc[kGU + i] = gload(us + (uint64_t)i * G);
         }
+    }
+    if (words) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t d = t + 256u * (uint32_t)k;
+            if (d < nd) {
+                sw[k] = *(const __attribute__((address_space(1))) uint32_t *)(gs + 4u * d);
+                sw[2 + k] = *(const __attribute__((address_space(1))) uint32_t *)(us + 4u * d);
+            }
+        }
+    }
+    if (g < G) {
         float xf[32];
         bf16x32_to_f32((const uint4 *)P.hidden_in + 4u * g, xf);
 #pragma unroll
-        for (int r = 0; r < 2 * kGU; r++) {
-            sm.part[r][wave][lane] = fp4_group(w[r], xf);
-            sm.scl[r][wave][lane] = e8m0_to_f32(sc[r]);
+        for (int r = 0; r < 2 * kGU; r++) sm.part[r][wave][lane] = fp4_group(w[r], xf);
+    }
+    uint8_t *sb = (uint8_t *)sm.scl;
+    if (words) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t d = t + 256u * (uint32_t)k;
+            if (d < nd) { /* byte 4 d: row 4 d / G, group 4 d % G (G % 4 == 0) */
+                const uint32_t r = 4u * d / G, c4 = (4u * d % G) / 4u;
+                sm.scl[r][c4] = sw[k];
+                sm.scl[kGU + r][c4] = sw[2 + k];
+            }
         }
+    } else if (g < G) {
+#pragma unroll
+        for (int r = 0; r < 2 * kGU; r++)
+            sb[256u * (uint32_t)r + g] = (uint8_t)gload((r < kGU ? gs + (uint64_t)r * G
+                                                                 : us + (uint64_t)(r - kGU) * G) + g);
     }
     __syncthreads();
     /* wave w: gate rows 2w, 2w+1 and the same up rows; lane l's groups
@@ -212,7 +241,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
         const int r = (q / RPW) * kGU + (int)wave * RPW + (q % RPW);
         float acc = 0.0f;
         for (uint32_t j = 0; j < stripes; j++)
-            if (64u * j + lane < G) acc = fmaf(sm.part[r][j][lane], sm.scl[r][j][lane], acc);
+            if (64u * j + lane < G)
+                acc = fmaf(sm.part[r][j][lane], e8m0_to_f32(sb[256u * (uint32_t)r + 64u * j + lane]), acc);
         p[q] = acc;
     }
     const float v = wave_sum_rows<2 * RPW>(p); /* lanes < 32: gate, lanes >= 32: up */
