@@ -129,6 +129,35 @@ def test_decode_layer_bitexact(cuda, cfg):
 
 
 
+@pytest.mark.parametrize("T", [1, 5])
+def test_missing_routes(cuda, T):
+    """Only two experts selectable (NaN bias elsewhere) with top_k = 4: the
+    last two slots of every token are missing (id UINT32_MAX, weight 0) and
+    contribute nothing. Decode (T = 1, whose top-k resolves descriptors
+    itself) and the batched path must both match the oracle run on the
+    two live routes with the top-k's own weights (the combine adds live
+    routes in rank order, so this is bit-exact)."""
+    import dataclasses
+    cfg = CONFIGS[0]
+    inputs = make_inputs(cfg, tokens=T, seed=cfg.seed + 5)
+    bias = np.full(cfg.experts, np.nan, np.float32)
+    bias[5], bias[40] = 0.01, -0.02
+    inputs = dataclasses.replace(inputs, router_bias=bias)
+    moe = get_layer(cfg, inputs, cuda)
+    out, ids, w = run(cfg, inputs, moe, cuda)
+    want_ids, want_w = O.router_topk(O.router_logits(inputs.router_weight, inputs.hidden), bias,
+                                     cfg.top_k, cfg.scale)
+    assert set(want_ids[:, :2].ravel().tolist()) <= {5, 40}
+    assert (want_ids[:, 2:] == 0xFFFFFFFF).all() and (want_w[:, 2:] == 0).all()
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(w, want_w)
+    live = dataclasses.replace(cfg, top_k=2)
+    want = O.layer(live, inputs, host_experts(moe.store, want_ids[:, :2]),
+                   ids=np.ascontiguousarray(want_ids[:, :2]),
+                   weights=np.ascontiguousarray(want_w[:, :2]))
+    np.testing.assert_array_equal(out, want["output"])
+
+
 @pytest.mark.parametrize("cfg_index,check", [(0, None), (2, 12), (3, 6)])
 def test_batched_layer_bitexact(cuda, cfg_index, check):
     cfg = CONFIGS[cfg_index]

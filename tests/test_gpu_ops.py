@@ -194,13 +194,19 @@ def test_router_topk_bitexact(cuda, E, k, scale):
     logits = rng.normal(0, 1.7, (T, E)).astype(np.float32)
     logits[0, :] = 0.25  # all-equal scores: ties broken by lower id
     logits[1, ::3] = logits[1, 0]  # many exact ties
+    logits[2, 3:] = np.nan  # NaN choices are never selected: fewer than k routes
+    logits[3, :] = np.nan  # nothing selectable: every slot missing
+    logits[4, :] = -np.inf  # score 0 everywhere: the bias decides
     bias = rng.normal(0, 0.01, E).astype(np.float32)
+    bias[::97] = -np.inf  # choice -inf is still selectable (after every finite one)
     ids = torch.zeros((T, k), dtype=torch.int32, device=cuda)
     w = torch.zeros((T, k), dtype=torch.float32, device=cuda)
     assert ops.k3_rocm_router_topk_f32_batch(ids, w, dev(logits, cuda), dev(bias, cuda), T, E, k,
                                              scale)
     sync()
     want_ids, want_w = O.router_topk(logits, bias, k, scale)
+    assert (want_ids[2, 3:] == 0xFFFFFFFF).all() and (want_w[2, 3:] == 0).all()
+    assert (want_ids[3] == 0xFFFFFFFF).all()
     np.testing.assert_array_equal(host(ids).view(np.uint32), want_ids)
     np.testing.assert_array_equal(host(w), want_w)
     # single-vector form
