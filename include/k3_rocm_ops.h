@@ -99,6 +99,91 @@ bool k3_rocm_bf16_gemm_tiled_f32(void       *output,
                                  uint32_t    batch_tile,
                                  void       *stream);
 
+/* k3_rocm_ops.h:82-87 / k3_rocm_ops.cu:1694-1703. bf16 [rows, columns]
+ * weights x bf16 input -> bf16: the bf16_gemv_f32 order rounded once. */
+bool k3_rocm_bf16_gemv_bf16(void       *output,
+                            const void *weights,
+                            const void *input,
+                            uint32_t    rows,
+                            uint32_t    columns,
+                            void       *stream);
+
+/* k3_rocm_ops.h:99-105 / k3_rocm_ops.cu:1760-1789. Per-row order identical
+ * to the GEMV for every vector. */
+bool k3_rocm_bf16_gemm_bf16(void       *output,
+                            const void *weights,
+                            const void *input,
+                            uint32_t    vector_count,
+                            uint32_t    rows,
+                            uint32_t    columns,
+                            void       *stream);
+
+/* k3_rocm_ops.h:89-97 / k3_rocm_ops.cu:1727-1758. batch_tile in {16, 32,
+ * 64}, otherwise false; results do not depend on it. */
+bool k3_rocm_bf16_gemm_tiled_bf16(void       *output,
+                                  const void *weights,
+                                  const void *input,
+                                  uint32_t    vector_count,
+                                  uint32_t    rows,
+                                  uint32_t    columns,
+                                  uint32_t    batch_tile,
+                                  void       *stream);
+
+/* k3_rocm_ops.h:138-144 / k3_rocm_ops.cu:1887-1908. Symmetric int8 in
+ * 128-element blocks: scale = max|w| / 127 (1 for an all-zero block), code
+ * = clamp(rint(w / scale), -127, 127), IEEE division, NaN codes as 0.
+ * quantized [rows, columns] int8, scales [rows, columns / 128] f32;
+ * columns % 128 == 0, weights 4-byte and quantized 2-byte aligned. */
+bool k3_rocm_bf16_quantize_q8_128(void       *quantized,
+                                  void       *scales,
+                                  const void *weights,
+                                  uint32_t    rows,
+                                  uint32_t    columns,
+                                  void       *stream);
+
+/* k3_rocm_ops.h:146-152 / k3_rocm_ops.cu:1910-1934. w = bf16(q * scale). */
+bool k3_rocm_q8_128_dequantize_bf16(void       *weights,
+                                    const void *quantized,
+                                    const void *scales,
+                                    uint32_t    rows,
+                                    uint32_t    columns,
+                                    void       *stream);
+
+/* k3_rocm_ops.h:154-161 / k3_rocm_ops.cu:1936-1946. Row order: lane l owns
+ * 32-column groups l, l + 64, ...; gs = fmaf(q, x, gs) over a group, acc =
+ * fmaf(gs, scale, acc); wave64 butterfly; bf16 round. columns % 128 == 0,
+ * quantized 8-byte, input 16-byte and scales 4-byte aligned. */
+bool k3_rocm_q8_128_gemv_bf16(void       *output,
+                              const void *quantized,
+                              const void *scales,
+                              const void *input,
+                              uint32_t    rows,
+                              uint32_t    columns,
+                              void       *stream);
+
+/* k3_rocm_ops.h:163-171 / k3_rocm_ops.cu:2007-2039. Per-row order identical
+ * to the GEMV for every vector. */
+bool k3_rocm_q8_128_gemm_bf16(void       *output,
+                              const void *quantized,
+                              const void *scales,
+                              const void *input,
+                              uint32_t    vector_count,
+                              uint32_t    rows,
+                              uint32_t    columns,
+                              void       *stream);
+
+/* k3_rocm_ops.h:173-182 / k3_rocm_ops.cu:1972-2005. batch_tile in {16, 32,
+ * 64}, otherwise false; results do not depend on it. */
+bool k3_rocm_q8_128_gemm_tiled_bf16(void       *output,
+                                    const void *quantized,
+                                    const void *scales,
+                                    const void *input,
+                                    uint32_t    vector_count,
+                                    uint32_t    rows,
+                                    uint32_t    columns,
+                                    uint32_t    batch_tile,
+                                    void       *stream);
+
 /* k3_rocm_ops.h:301-307 / k3_rocm_ops.cu:2399-2418. Latent RMSNorm of the
  * K3-native MoE tail. */
 bool k3_rocm_rms_norm_bf16(void       *output,

@@ -65,6 +65,14 @@ SIGNATURES = {
     "k3_rocm_bf16_gemm_f32": (_b, [_p, _p, _p, _u32, _u32, _u32, _p]),
     "k3_rocm_bf16_gemm_tiled_f32": (_b, [_p, _p, _p, _u32, _u32, _u32, _u32, _p]),
     "k3_rocm_rms_norm_bf16": (_b, [_p, _p, _p, _u32, _u32, _f, _p]),
+    "k3_rocm_bf16_gemv_bf16": (_b, [_p, _p, _p, _u32, _u32, _p]),
+    "k3_rocm_bf16_gemm_bf16": (_b, [_p, _p, _p, _u32, _u32, _u32, _p]),
+    "k3_rocm_bf16_gemm_tiled_bf16": (_b, [_p, _p, _p, _u32, _u32, _u32, _u32, _p]),
+    "k3_rocm_bf16_quantize_q8_128": (_b, [_p, _p, _p, _u32, _u32, _p]),
+    "k3_rocm_q8_128_dequantize_bf16": (_b, [_p, _p, _p, _u32, _u32, _p]),
+    "k3_rocm_q8_128_gemv_bf16": (_b, [_p, _p, _p, _p, _u32, _u32, _p]),
+    "k3_rocm_q8_128_gemm_bf16": (_b, [_p, _p, _p, _p, _u32, _u32, _u32, _p]),
+    "k3_rocm_q8_128_gemm_tiled_bf16": (_b, [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _p]),
     "k3_rocm_router_topk_f32": (_b, [_p, _p, _p, _p, _u32, _u32, _f, _p]),
     "k3_rocm_router_topk_f32_batch": (_b, [_p, _p, _p, _p, _u32, _u32, _u32, _f, _p]),
     "k3_rocm_weighted_sum_bf16": (_b, [_p, _p, _p, _u32, _u32, _p]),

@@ -12,6 +12,11 @@ bool launch_bf16_rows_f32_any(float *out, const void *weights, const void *input
                               uint32_t tokens, uint32_t rows, uint32_t cols,
                               hipStream_t stream);
 
+/* The same order with bf16 [tokens, rows] output (rounded once). */
+bool launch_bf16_rows_bf16_any(uint16_t *out, const void *weights, const void *input,
+                               uint32_t tokens, uint32_t rows, uint32_t cols,
+                               hipStream_t stream);
+
 /* Router top-k; ids2/w2 (nullable) receive extra copies (e.g. mapped host
  * memory) while ids/w stay in device memory for later kernels. */
 bool launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,

@@ -10,6 +10,10 @@
  *   MXFP4 rows: lane l owns 32-column groups l, l+64, ...; each group is
  *     gs = fmaf(e2m1, x, gs) over its 32 columns, then acc = fmaf(gs,
  *     2^(e-127), acc); wave64 butterfly; bf16 round.
+ *   Q8-128 rows: the MXFP4 skeleton with int8 codes: gs = fmaf(q, x, gs)
+ *     over a 32-column group (each product exact), acc = fmaf(gs,
+ *     scale[group / 4], acc); wave64 butterfly; bf16 round.
+ *   bf16 -> bf16 rows: the bf16 -> f32 order, rounded once to bf16.
  * Every token row of a batch uses the same order as the single-vector form,
  * so batch == sequential and results do not depend on the batch tile.
  */
@@ -37,9 +41,9 @@ inline uint32_t grid_cap(uint64_t blocks) {
 /* bf16 weights x bf16 inputs -> f32 (router logits)                         */
 /* ------------------------------------------------------------------------ */
 
-template <int TT>
+template <int TT, bool B16 = false>
 __global__ __launch_bounds__(256) void bf16_rows_f32_kernel(
-        float *__restrict__ out, const uint16_t *__restrict__ weights,
+        void *__restrict__ out, const uint16_t *__restrict__ weights,
         const uint16_t *__restrict__ input, uint32_t tokens, uint32_t rows,
         uint32_t cols, uint32_t vec_ok) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -85,18 +89,22 @@ __global__ __launch_bounds__(256) void bf16_rows_f32_kernel(
     }
     const float v = wave_sum_rows<TT>(acc);
     const int owner = wave_rows_owner<TT>();
-    if ((lane & (64u / TT - 1u)) == 0u && (uint32_t)owner < active)
-        out[(uint64_t)(t0 + owner) * rows + row] = v;
+    if ((lane & (64u / TT - 1u)) == 0u && (uint32_t)owner < active) {
+        const uint64_t o = (uint64_t)(t0 + owner) * rows + row;
+        if constexpr (B16)
+            ((uint16_t *)out)[o] = f32_to_bf16(v);
+        else
+            ((float *)out)[o] = v;
+    }
 }
 
-template <int TT>
+template <int TT, bool B16 = false>
 bool launch_bf16_rows_f32(void *out, const void *w, const void *x, uint32_t tokens,
                           uint32_t rows, uint32_t cols, hipStream_t s) {
     const uint32_t vec_ok = (cols % 8u == 0u) && (((uintptr_t)w | (uintptr_t)x) % 16u == 0u);
     dim3 grid((rows + kWavesPerBlock - 1u) / kWavesPerBlock, (tokens + TT - 1u) / TT);
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(bf16_rows_f32_kernel<TT>), grid, dim3(kThreads), 0, s,
-                       (float *)out, (const uint16_t *)w, (const uint16_t *)x, tokens, rows,
-                       cols, vec_ok);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(bf16_rows_f32_kernel<TT, B16>), grid, dim3(kThreads), 0, s,
+                       out, (const uint16_t *)w, (const uint16_t *)x, tokens, rows, cols, vec_ok);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -124,8 +132,9 @@ bool launch_bf16_rows_f32(void *out, const void *w, const void *x, uint32_t toke
 constexpr int kGT = 32, kGE = 16, kGThreads = 512;
 constexpr uint32_t kGemmMinTokens = 128;
 
+template <bool B16>
 __global__ __launch_bounds__(512) void bf16_gemm_w64_kernel(
-        float *__restrict__ out, const uint16_t *__restrict__ weights,
+        void *__restrict__ out, const uint16_t *__restrict__ weights,
         const uint16_t *__restrict__ input, uint32_t tokens, uint32_t rows, uint32_t cols,
         uint32_t row_tiles, uint32_t xcd_groups) {
     __shared__ float4 xs[2][kGT][64];
@@ -221,10 +230,16 @@ __global__ __launch_bounds__(512) void bf16_gemm_w64_kernel(
     const int owner = wave_rows_owner<64>();
     const uint32_t t = t0 + 8u * wt + (uint32_t)(owner >> 3);
     const uint32_t e = e0 + 8u * we + (uint32_t)(owner & 7);
-    if (t < tokens && e < rows) out[(uint64_t)t * rows + e] = v;
+    if (t < tokens && e < rows) {
+        if constexpr (B16)
+            ((uint16_t *)out)[(uint64_t)t * rows + e] = f32_to_bf16(v);
+        else
+            ((float *)out)[(uint64_t)t * rows + e] = v;
+    }
 }
 
-bool launch_bf16_gemm_w64(float *out, const void *w, const void *x, uint32_t tokens,
+template <bool B16>
+bool launch_bf16_gemm_w64(void *out, const void *w, const void *x, uint32_t tokens,
                           uint32_t rows, uint32_t cols, hipStream_t s) {
     const uint32_t token_tiles = (tokens + kGT - 1u) / kGT;
     const uint32_t row_tiles = (rows + kGE - 1u) / kGE;
@@ -232,7 +247,7 @@ bool launch_bf16_gemm_w64(float *out, const void *w, const void *x, uint32_t tok
     const uint64_t blocks = xcd ? 8ull * token_tiles * ((row_tiles + 7u) / 8u)
                                 : (uint64_t)token_tiles * row_tiles;
     if (blocks > 0x7fffffffull) return false;
-    hipLaunchKernelGGL(bf16_gemm_w64_kernel, dim3((uint32_t)blocks), dim3(kGThreads), 0, s, out,
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(bf16_gemm_w64_kernel<B16>), dim3((uint32_t)blocks), dim3(kGThreads), 0, s, out,
                        (const uint16_t *)w, (const uint16_t *)x, tokens, rows, cols, row_tiles,
                        xcd);
     return hipGetLastError() == hipSuccess;
@@ -328,6 +343,118 @@ bool launch_mxfp4_rows(void *out, const void *p, const void *s, const void *x,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Q8-128 static projections                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* 32 int8 codes of a group: 16-byte aligned rows load two uint4, 8-byte
+ * aligned ones four uint2 (the reference reads 8-byte octets). */
+__device__ __forceinline__ void load_q8_group(const int8_t *p, uint32_t align16, uint4 &a,
+                                              uint4 &b) {
+    if (align16) {
+        a = ((const uint4 *)p)[0];
+        b = ((const uint4 *)p)[1];
+        return;
+    }
+    const uint2 *q = (const uint2 *)p;
+    const uint2 c0 = q[0], c1 = q[1], c2 = q[2], c3 = q[3];
+    a = make_uint4(c0.x, c0.y, c1.x, c1.y);
+    b = make_uint4(c2.x, c2.y, c3.x, c3.y);
+}
+
+/* gs = fmaf(q_i, x_i, gs) over the group's 32 columns in order. */
+__device__ __forceinline__ float q8_group(const uint4 &a, const uint4 &b, const float *x) {
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float gs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            gs = fmaf((float)(int8_t)(w[k] >> (8 * i)), x[4 * k + i], gs);
+    return gs;
+}
+
+/* One wave per row (tokens in tiles of TT); order in the file header. */
+template <int TT>
+__global__ __launch_bounds__(256) void q8_rows_kernel(
+        uint16_t *__restrict__ out, const int8_t *__restrict__ codes,
+        const float *__restrict__ scales, const uint16_t *__restrict__ input,
+        uint32_t tokens, uint32_t rows, uint32_t cols, uint32_t align16) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const uint32_t t0 = blockIdx.y * TT;
+    if (row >= rows) return;
+    const uint32_t active = tokens - t0 < (uint32_t)TT ? tokens - t0 : (uint32_t)TT;
+    const uint32_t groups = cols / 32u;
+    const int8_t *qrow = codes + (uint64_t)row * cols;
+    const float *srow = scales + (uint64_t)row * (cols / 128u);
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = 0.0f;
+    for (uint32_t g = lane; g < groups; g += 64u) {
+        uint4 a, b;
+        load_q8_group(qrow + 32u * g, align16, a, b);
+        const float sc = srow[g >> 2];
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            if ((uint32_t)t < active) {
+                float xf[32];
+                bf16x32_to_f32((const uint4 *)(input + (uint64_t)(t0 + t) * cols) + 4u * g, xf);
+                acc[t] = fmaf(q8_group(a, b, xf), sc, acc[t]);
+            }
+        }
+    }
+    const float v = wave_sum_rows<TT>(acc);
+    const int owner = wave_rows_owner<TT>();
+    if ((lane & (64u / TT - 1u)) == 0u && (uint32_t)owner < active)
+        out[(uint64_t)(t0 + owner) * rows + row] = f32_to_bf16(v);
+}
+
+template <int TT>
+bool launch_q8_rows(void *out, const void *q, const void *s, const void *x, uint32_t tokens,
+                    uint32_t rows, uint32_t cols, hipStream_t st) {
+    const uint32_t align16 = ((uintptr_t)q % 16u) == 0u;
+    dim3 grid((rows + kWavesPerBlock - 1u) / kWavesPerBlock, (tokens + TT - 1u) / TT);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_rows_kernel<TT>), grid, dim3(kThreads), 0, st,
+                       (uint16_t *)out, (const int8_t *)q, (const float *)s, (const uint16_t *)x,
+                       tokens, rows, cols, align16);
+    return hipGetLastError() == hipSuccess;
+}
+
+/* One wave per 128-element block: scale = max|w| / 127 (1 for an all-zero
+ * block), code = clamp(rint(w / scale), -127, 127) with IEEE division;
+ * a NaN weight codes as 0 (k3_rocm_ops.cu:662-697). */
+__global__ __launch_bounds__(256) void q8_quantize_kernel(int8_t *__restrict__ codes,
+                                                          float *__restrict__ scales,
+                                                          const uint16_t *__restrict__ w,
+                                                          uint64_t blocks) {
+    const uint64_t blk = (uint64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (blk >= blocks) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t pair = ((const uint32_t *)(w + 128u * blk))[lane];
+    const float v0 = bf16_lo(pair), v1 = bf16_hi(pair);
+    float m = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float sc = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    auto code = [&](float v) -> uint32_t {
+        float r = rintf(__fdiv_rn(v, sc));
+        if (r != r) r = 0.0f;
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        return (uint32_t)(uint8_t)(int8_t)(int)r;
+    };
+    ((uint16_t *)(codes + 128u * blk))[lane] = (uint16_t)(code(v0) | (code(v1) << 8));
+    if (lane == 0u) scales[blk] = sc;
+}
+
+/* w = bf16(q * scale) (k3_rocm_ops.cu:699-711). */
+__global__ void q8_dequantize_kernel(uint16_t *__restrict__ w, const int8_t *__restrict__ codes,
+                                     const float *__restrict__ scales, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)blockDim.x * gridDim.x)
+        w[i] = f32_to_bf16(__fmul_rn((float)codes[i], scales[i / 128u]));
+}
+
+/* ------------------------------------------------------------------------ */
 /* elementwise                                                               */
 /* ------------------------------------------------------------------------ */
 
@@ -396,14 +523,27 @@ __global__ void rms_norm_kernel(uint16_t *__restrict__ out, const uint16_t *__re
 
 }  // namespace
 
-bool k3::launch_bf16_rows_f32_any(float *out, const void *w, const void *x, uint32_t tokens,
-                                  uint32_t rows, uint32_t cols, hipStream_t s) {
-    if (tokens == 1u) return launch_bf16_rows_f32<1>(out, w, x, 1u, rows, cols, s);
-    if (tokens <= 4u) return launch_bf16_rows_f32<4>(out, w, x, tokens, rows, cols, s);
+namespace {
+template <bool B16>
+bool launch_bf16_rows_any(void *out, const void *w, const void *x, uint32_t tokens,
+                          uint32_t rows, uint32_t cols, hipStream_t s) {
+    if (tokens == 1u) return launch_bf16_rows_f32<1, B16>(out, w, x, 1u, rows, cols, s);
+    if (tokens <= 4u) return launch_bf16_rows_f32<4, B16>(out, w, x, tokens, rows, cols, s);
     /* many tokens: the blocked GEMM (same bits); it needs 16-byte rows */
     if (tokens >= kGemmMinTokens && cols % 8u == 0u && ((uintptr_t)w | (uintptr_t)x) % 16u == 0u)
-        return launch_bf16_gemm_w64(out, w, x, tokens, rows, cols, s);
-    return launch_bf16_rows_f32<16>(out, w, x, tokens, rows, cols, s);
+        return launch_bf16_gemm_w64<B16>(out, w, x, tokens, rows, cols, s);
+    return launch_bf16_rows_f32<16, B16>(out, w, x, tokens, rows, cols, s);
+}
+}  // namespace
+
+bool k3::launch_bf16_rows_f32_any(float *out, const void *w, const void *x, uint32_t tokens,
+                                  uint32_t rows, uint32_t cols, hipStream_t s) {
+    return launch_bf16_rows_any<false>(out, w, x, tokens, rows, cols, s);
+}
+
+bool k3::launch_bf16_rows_bf16_any(uint16_t *out, const void *w, const void *x, uint32_t tokens,
+                                   uint32_t rows, uint32_t cols, hipStream_t s) {
+    return launch_bf16_rows_any<true>(out, w, x, tokens, rows, cols, s);
 }
 
 bool k3::launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,
@@ -598,4 +738,107 @@ extern "C" bool k3_rocm_rms_norm_bf16(void *output, const void *input, const voi
                        (uint16_t *)output, (const uint16_t *)input, (const uint16_t *)weight,
                        hidden_size, epsilon);
     return hipGetLastError() == hipSuccess;
+}
+
+/* ------------------------------------------------------------------------ */
+/* bf16 -> bf16 and Q8-128 static projections                                */
+/* ------------------------------------------------------------------------ */
+
+extern "C" bool k3_rocm_bf16_gemm_tiled_bf16(void *output, const void *weights,
+                                             const void *input, uint32_t vector_count,
+                                             uint32_t rows, uint32_t columns,
+                                             uint32_t batch_tile, void *stream) {
+    if (!output || !weights || !input || vector_count == 0u || vector_count > 65535u ||
+        rows == 0u || columns == 0u)
+        return false;
+    const hipStream_t s = (hipStream_t)stream;
+    switch (batch_tile) {
+        case 16u: return launch_bf16_rows_f32<16, true>(output, weights, input, vector_count, rows, columns, s);
+        case 32u: return launch_bf16_rows_f32<32, true>(output, weights, input, vector_count, rows, columns, s);
+        case 64u: return launch_bf16_rows_f32<64, true>(output, weights, input, vector_count, rows, columns, s);
+        default: return false;
+    }
+}
+
+extern "C" bool k3_rocm_bf16_gemm_bf16(void *output, const void *weights, const void *input,
+                                       uint32_t vector_count, uint32_t rows, uint32_t columns,
+                                       void *stream) {
+    if (!output || !weights || !input || vector_count == 0u || vector_count > 65535u ||
+        rows == 0u || columns == 0u)
+        return false;
+    return k3::launch_bf16_rows_bf16_any((uint16_t *)output, weights, input, vector_count, rows,
+                                         columns, (hipStream_t)stream);
+}
+
+extern "C" bool k3_rocm_bf16_gemv_bf16(void *output, const void *weights, const void *input,
+                                       uint32_t rows, uint32_t columns, void *stream) {
+    return k3_rocm_bf16_gemm_bf16(output, weights, input, 1u, rows, columns, stream);
+}
+
+extern "C" bool k3_rocm_bf16_quantize_q8_128(void *quantized, void *scales, const void *weights,
+                                             uint32_t rows, uint32_t columns, void *stream) {
+    if (!quantized || !scales || !weights || rows == 0u || columns == 0u || columns % 128u != 0u ||
+        ((uintptr_t)weights % 4u) != 0u || ((uintptr_t)quantized % 2u) != 0u)
+        return false;
+    const uint64_t blocks = (uint64_t)rows * (columns / 128u);
+    const uint64_t grid = (blocks + kWavesPerBlock - 1u) / kWavesPerBlock;
+    if (grid > 0x7fffffffull) return false;
+    hipLaunchKernelGGL(q8_quantize_kernel, dim3((uint32_t)grid), dim3(kThreads), 0,
+                       (hipStream_t)stream, (int8_t *)quantized, (float *)scales,
+                       (const uint16_t *)weights, blocks);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_rocm_q8_128_dequantize_bf16(void *weights, const void *quantized,
+                                               const void *scales, uint32_t rows,
+                                               uint32_t columns, void *stream) {
+    if (!weights || !quantized || !scales || rows == 0u || columns == 0u || columns % 128u != 0u)
+        return false;
+    const uint64_t n = (uint64_t)rows * columns;
+    hipLaunchKernelGGL(q8_dequantize_kernel, dim3(grid_cap((n + 255u) / 256u)), dim3(256), 0,
+                       (hipStream_t)stream, (uint16_t *)weights, (const int8_t *)quantized,
+                       (const float *)scales, n);
+    return hipGetLastError() == hipSuccess;
+}
+
+static bool q8_args_ok(const void *output, const void *quantized, const void *scales,
+                       const void *input, uint32_t vector_count, uint32_t rows,
+                       uint32_t columns) {
+    return output && quantized && scales && input && vector_count != 0u &&
+           vector_count <= 65535u && rows != 0u && columns != 0u && columns % 128u == 0u &&
+           ((uintptr_t)quantized % 8u) == 0u && ((uintptr_t)input % 16u) == 0u &&
+           ((uintptr_t)scales % 4u) == 0u;
+}
+
+extern "C" bool k3_rocm_q8_128_gemm_tiled_bf16(void *output, const void *quantized,
+                                               const void *scales, const void *input,
+                                               uint32_t vector_count, uint32_t rows,
+                                               uint32_t columns, uint32_t batch_tile,
+                                               void *stream) {
+    if (!q8_args_ok(output, quantized, scales, input, vector_count, rows, columns)) return false;
+    const hipStream_t s = (hipStream_t)stream;
+    switch (batch_tile) {
+        case 16u: return launch_q8_rows<16>(output, quantized, scales, input, vector_count, rows, columns, s);
+        case 32u: return launch_q8_rows<32>(output, quantized, scales, input, vector_count, rows, columns, s);
+        case 64u: return launch_q8_rows<64>(output, quantized, scales, input, vector_count, rows, columns, s);
+        default: return false;
+    }
+}
+
+extern "C" bool k3_rocm_q8_128_gemm_bf16(void *output, const void *quantized, const void *scales,
+                                         const void *input, uint32_t vector_count, uint32_t rows,
+                                         uint32_t columns, void *stream) {
+    if (!q8_args_ok(output, quantized, scales, input, vector_count, rows, columns)) return false;
+    const hipStream_t s = (hipStream_t)stream;
+    if (vector_count == 1u)
+        return launch_q8_rows<1>(output, quantized, scales, input, 1u, rows, columns, s);
+    if (vector_count <= 4u)
+        return launch_q8_rows<4>(output, quantized, scales, input, vector_count, rows, columns, s);
+    return launch_q8_rows<16>(output, quantized, scales, input, vector_count, rows, columns, s);
+}
+
+extern "C" bool k3_rocm_q8_128_gemv_bf16(void *output, const void *quantized, const void *scales,
+                                         const void *input, uint32_t rows, uint32_t columns,
+                                         void *stream) {
+    return k3_rocm_q8_128_gemm_bf16(output, quantized, scales, input, 1u, rows, columns, stream);
 }

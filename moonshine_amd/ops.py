@@ -72,6 +72,52 @@ def k3_rocm_rms_norm_bf16(output, input, weight, vector_count, hidden_size, epsi
                                        hidden_size, epsilon, _stream(stream))
 
 
+def k3_rocm_bf16_gemv_bf16(output, weights, input, rows, columns, stream=None):
+    return lib().k3_rocm_bf16_gemv_bf16(_ptr(output), _ptr(weights), _ptr(input), rows, columns,
+                                        _stream(stream))
+
+
+def k3_rocm_bf16_gemm_bf16(output, weights, input, vector_count, rows, columns, stream=None):
+    return lib().k3_rocm_bf16_gemm_bf16(_ptr(output), _ptr(weights), _ptr(input), vector_count,
+                                        rows, columns, _stream(stream))
+
+
+def k3_rocm_bf16_gemm_tiled_bf16(output, weights, input, vector_count, rows, columns,
+                                 batch_tile, stream=None):
+    return lib().k3_rocm_bf16_gemm_tiled_bf16(_ptr(output), _ptr(weights), _ptr(input),
+                                              vector_count, rows, columns, batch_tile,
+                                              _stream(stream))
+
+
+def k3_rocm_bf16_quantize_q8_128(quantized, scales, weights, rows, columns, stream=None):
+    return lib().k3_rocm_bf16_quantize_q8_128(_ptr(quantized), _ptr(scales), _ptr(weights), rows,
+                                              columns, _stream(stream))
+
+
+def k3_rocm_q8_128_dequantize_bf16(weights, quantized, scales, rows, columns, stream=None):
+    return lib().k3_rocm_q8_128_dequantize_bf16(_ptr(weights), _ptr(quantized), _ptr(scales),
+                                                rows, columns, _stream(stream))
+
+
+def k3_rocm_q8_128_gemv_bf16(output, quantized, scales, input, rows, columns, stream=None):
+    return lib().k3_rocm_q8_128_gemv_bf16(_ptr(output), _ptr(quantized), _ptr(scales),
+                                          _ptr(input), rows, columns, _stream(stream))
+
+
+def k3_rocm_q8_128_gemm_bf16(output, quantized, scales, input, vector_count, rows, columns,
+                             stream=None):
+    return lib().k3_rocm_q8_128_gemm_bf16(_ptr(output), _ptr(quantized), _ptr(scales),
+                                          _ptr(input), vector_count, rows, columns,
+                                          _stream(stream))
+
+
+def k3_rocm_q8_128_gemm_tiled_bf16(output, quantized, scales, input, vector_count, rows,
+                                   columns, batch_tile, stream=None):
+    return lib().k3_rocm_q8_128_gemm_tiled_bf16(_ptr(output), _ptr(quantized), _ptr(scales),
+                                                _ptr(input), vector_count, rows, columns,
+                                                batch_tile, _stream(stream))
+
+
 def k3_rocm_router_topk_f32(expert_ids, expert_weights, logits, correction_bias, expert_count,
                             top_k, scaling_factor, stream=None):
     return lib().k3_rocm_router_topk_f32(_ptr(expert_ids), _ptr(expert_weights), _ptr(logits),

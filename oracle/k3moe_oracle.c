@@ -506,6 +506,143 @@ void k3o_mxfp4_gemm(uint16_t *out, float *out_f32, const uint8_t *packed,
     }
 }
 
+/* ---- Q8-128 static projections ------------------------------------------ */
+
+/* k3_rocm_ops.cu:662-697: per 128-element block, scale = max|w| / 127 (1 for
+ * an all-zero block), code = clamp(rint(w / scale), -127, 127). Division
+ * here is IEEE (the reference builds with fast math); a NaN codes as 0. */
+void k3o_q8_quantize(int8_t *q, float *scales, const uint16_t *w,
+                     uint32_t rows, uint32_t cols) {
+    const uint64_t blocks = (uint64_t)rows * (cols / 128u);
+    for (uint64_t b = 0; b < blocks; b++) {
+        const uint16_t *x = w + 128u * b;
+        float m = 0.0f;
+        for (uint32_t i = 0; i < 128u; i++) m = fmaxf(m, fabsf(k3o_bf16_to_f32(x[i])));
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        scales[b] = sc;
+        for (uint32_t i = 0; i < 128u; i++) {
+            float r = rintf(k3o_bf16_to_f32(x[i]) / sc);
+            if (r != r) r = 0.0f;
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            q[128u * b + i] = (int8_t)(int)r;
+        }
+    }
+}
+
+/* k3_rocm_ops.cu:699-711: w = bf16(q * scale). */
+void k3o_q8_dequantize(uint16_t *w, const int8_t *q, const float *scales,
+                       uint32_t rows, uint32_t cols) {
+    const uint64_t n = (uint64_t)rows * cols;
+    for (uint64_t i = 0; i < n; i++)
+        w[i] = k3o_f32_to_bf16((float)q[i] * scales[i / 128u]);
+}
+
+/* w64: lane l owns 32-column groups l, l+64, ...; gs = fmaf(q, x, gs) over
+ * the group in column order (products exact), acc = fmaf(gs, scale, acc);
+ * butterfly64. */
+static float q8_row_w64(const int8_t *q, const float *s, const uint16_t *x, uint32_t cols) {
+    float lane[64];
+    const uint32_t groups = cols / 32u;
+    for (uint32_t l = 0; l < 64u; l++) {
+        float acc = 0.0f;
+        for (uint32_t g = l; g < groups; g += 64u) {
+            float gs = 0.0f;
+            for (uint32_t i = 32u * g; i < 32u * g + 32u; i++)
+                gs = fmaf((float)q[i], k3o_bf16_to_f32(x[i]), gs);
+            acc = fmaf(gs, s[g / 4u], acc);
+        }
+        lane[l] = acc;
+    }
+    return butterfly64(lane);
+}
+
+/* Reference order, k3_rocm_ops.cu:713-751: 256 threads, thread t sums the
+ * octets t, t+256, ... as partial += (q * scale) * x (as written), then the
+ * LDS tree. Tolerance checks only (fast-math build). */
+static float q8_row_ref256(const int8_t *q, const float *s, const uint16_t *x, uint32_t cols) {
+    float p[256];
+    const uint32_t octets = cols / 8u;
+    for (uint32_t t = 0; t < 256u; t++) {
+        float partial = 0.0f;
+        for (uint32_t o = t; o < octets; o += 256u) {
+            const float sc = s[o / 16u];
+            for (uint32_t i = 8u * o; i < 8u * o + 8u; i++)
+                partial += ((float)q[i] * sc) * k3o_bf16_to_f32(x[i]);
+        }
+        p[t] = partial;
+    }
+    return tree_reduce(p, 256u);
+}
+
+static double q8_row_f64(const int8_t *q, const float *s, const uint16_t *x, uint32_t cols) {
+    double acc = 0.0;
+    for (uint32_t i = 0; i < cols; i++)
+        acc += (double)q[i] * (double)s[i / 128u] * (double)k3o_bf16_to_f32(x[i]);
+    return acc;
+}
+
+void k3o_q8_gemm(uint16_t *out, float *out_f32, const int8_t *q,
+                 const float *scales, const uint16_t *input, uint32_t vectors,
+                 uint32_t rows, uint32_t cols, int order) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t t = 0; t < (int64_t)vectors; t++) {
+        for (int64_t r = 0; r < (int64_t)rows; r++) {
+            const int8_t *qr = q + (uint64_t)r * cols;
+            const float *sr = scales + (uint64_t)r * (cols / 128u);
+            const uint16_t *x = input + (uint64_t)t * cols;
+            float v;
+            if (order == 0) v = q8_row_w64(qr, sr, x, cols);
+            else if (order == 1) v = q8_row_ref256(qr, sr, x, cols);
+            else v = (float)q8_row_f64(qr, sr, x, cols);
+            const uint64_t o = (uint64_t)t * rows + r;
+            if (out) out[o] = k3o_f32_to_bf16(v);
+            if (out_f32) out_f32[o] = v;
+        }
+    }
+}
+
+/* ---- RMSNorm (k3_rocm_ops.cu:837-867) ------------------------------------- */
+
+void k3o_rms_norm(uint16_t *out, const uint16_t *in, const uint16_t *weight,
+                  uint32_t vectors, uint32_t hidden, float eps, int order) {
+    for (uint32_t v = 0; v < vectors; v++) {
+        const uint16_t *x = in + (uint64_t)v * hidden;
+        uint16_t *o = out + (uint64_t)v * hidden;
+        float p[256];
+        for (uint32_t t = 0; t < 256u; t++) {
+            float acc = 0.0f;
+            for (uint32_t d = t; d < hidden; d += 256u) {
+                const float e = k3o_bf16_to_f32(x[d]);
+                acc = order == 0 ? fmaf(e, e, acc) : acc + e * e;
+            }
+            p[t] = acc;
+        }
+        if (order == 2) {
+            double ss = 0.0;
+            for (uint32_t d = 0; d < hidden; d++) {
+                const double e = k3o_bf16_to_f32(x[d]);
+                ss += e * e;
+            }
+            const double inv = 1.0 / sqrt(ss / hidden + (double)eps);
+            for (uint32_t d = 0; d < hidden; d++)
+                o[d] = k3o_f32_to_bf16((float)((double)k3o_bf16_to_f32(x[d]) * inv *
+                                               (double)k3o_bf16_to_f32(weight[d])));
+            continue;
+        }
+        float total;
+        if (order == 0) {
+            float w[4];
+            for (int q = 0; q < 4; q++) w[q] = butterfly64(p + 64 * q);
+            total = (w[0] + w[1]) + (w[2] + w[3]);
+        } else {
+            total = tree_reduce(p, 256u);
+        }
+        const float inv = 1.0f / sqrtf(total / (float)hidden + eps);
+        for (uint32_t d = 0; d < hidden; d++)
+            o[d] = k3o_f32_to_bf16((k3o_bf16_to_f32(x[d]) * inv) * k3o_bf16_to_f32(weight[d]));
+    }
+}
+
 /* ---- combine ------------------------------------------------------------- */
 
 /* k3_rocm_ops.cu:1452-1474: sum starts at 0 and adds w[r] * y[r] in rank

@@ -87,6 +87,22 @@ void k3o_bf16_gemm_f32(float *out, const uint16_t *weights,
                        const uint16_t *input, uint32_t vectors,
                        uint32_t rows, uint32_t columns, int order);
 
+/* ---- static projections of the K3-native tail (k3_rocm_ops.cu:662-867) - */
+/* Q8-128: int8 codes [rows, cols], f32 scales [rows, cols / 128]. */
+void k3o_q8_quantize(int8_t *q, float *scales, const uint16_t *w,
+                     uint32_t rows, uint32_t cols);
+void k3o_q8_dequantize(uint16_t *w, const int8_t *q, const float *scales,
+                       uint32_t rows, uint32_t cols);
+/* order: 0 = w64, 1 = reference 256-thread, 2 = fp64 (out_f32) */
+void k3o_q8_gemm(uint16_t *out, float *out_f32, const int8_t *q,
+                 const float *scales, const uint16_t *input, uint32_t vectors,
+                 uint32_t rows, uint32_t cols, int order);
+/* order: 0 = the library's (256-thread strided fmaf, per-wave butterfly,
+ * (w0 + w1) + (w2 + w3), IEEE 1/sqrt), 1 = reference 256-thread tree,
+ * 2 = fp64 */
+void k3o_rms_norm(uint16_t *out, const uint16_t *in, const uint16_t *weight,
+                  uint32_t vectors, uint32_t hidden, float eps, int order);
+
 /* ---- combine (k3_rocm_ops.cu:1452-1510) -------------------------------- */
 void k3o_weighted_sum(uint16_t *out, const uint16_t *vectors,
                       const float *weights, uint32_t tokens,

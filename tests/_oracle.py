@@ -71,6 +71,10 @@ def lib():
             "k3o_f32_to_e4m3": (ctypes.c_uint8, [_f]),
             "k3o_mx8_quantize": (None, [_p, _p, _p, _u64]),
             "k3o_mx8_split": (None, [_p, _p, _p, _p, _p, _u64]),
+            "k3o_q8_quantize": (None, [_p, _p, _p, _u32, _u32]),
+            "k3o_q8_dequantize": (None, [_p, _p, _p, _u32, _u32]),
+            "k3o_q8_gemm": (None, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _i]),
+            "k3o_rms_norm": (None, [_p, _p, _p, _u32, _u32, _f, _i]),
         }
         for n, (r, a) in sig.items():
             fn = getattr(L, n)
@@ -128,6 +132,47 @@ def bf16_gemm_f32(w, x, order=ORDER_W64):
     T = x.shape[0]
     out = np.empty((T, rows), np.float32)
     lib().k3o_bf16_gemm_f32(_ptr(out), _ptr(w), _ptr(x), T, rows, cols, order)
+    return out
+
+
+def bf16_gemm_bf16(w, x, order=ORDER_W64):
+    """bf16 output of the bf16 -> f32 order, rounded once."""
+    from moonshine_amd.synth import f32_to_bf16_bits
+    return f32_to_bf16_bits(bf16_gemm_f32(w, x, order))
+
+
+def q8_quantize(w):
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty((rows, cols // 128), np.float32)
+    lib().k3o_q8_quantize(_ptr(q), _ptr(s), _ptr(np.ascontiguousarray(w)), rows, cols)
+    return q, s
+
+
+def q8_dequantize(q, s):
+    rows, cols = q.shape
+    w = np.empty((rows, cols), np.uint16)
+    lib().k3o_q8_dequantize(_ptr(w), _ptr(np.ascontiguousarray(q)), _ptr(np.ascontiguousarray(s)),
+                            rows, cols)
+    return w
+
+
+def q8_gemm(q, s, x, order=ORDER_W64):
+    rows, cols = q.shape
+    T = x.shape[0]
+    out = np.empty((T, rows), np.uint16)
+    f = np.empty((T, rows), np.float32)
+    lib().k3o_q8_gemm(_ptr(out), _ptr(f), _ptr(np.ascontiguousarray(q)),
+                      _ptr(np.ascontiguousarray(s)), _ptr(np.ascontiguousarray(x)), T, rows, cols,
+                      order)
+    return out, f
+
+
+def rms_norm(x, w, eps=1e-5, order=ORDER_W64):
+    T, H = x.shape
+    out = np.empty((T, H), np.uint16)
+    lib().k3o_rms_norm(_ptr(out), _ptr(np.ascontiguousarray(x)), _ptr(np.ascontiguousarray(w)), T,
+                       H, eps, order)
     return out
 
 

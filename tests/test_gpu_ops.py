@@ -299,3 +299,95 @@ def test_against_reference_kernels(cuda):
     _, f64 = O.mxfp4_gemm(p, s, x, rows, cols, O.ORDER_F64)
     scale = np.maximum(np.abs(f64[0]), 1.0)
     assert np.max(np.abs(a - b) / scale) <= 2 * 2.0 ** -8
+
+
+# ---- static projections of the K3-native tail -------------------------------
+
+@pytest.mark.parametrize("T,rows,cols", [(1, 3584, 7168), (3, 96, 1000), (17, 64, 3584),
+                                         (130, 40, 2048)])
+def test_bf16_gemm_bf16_bitexact(cuda, T, rows, cols):
+    rng = np.random.default_rng(rows + cols + T)
+    w = rand_bf16(rng, (rows, cols), 0.02)
+    x = rand_bf16(rng, (T, cols))
+    want = O.bf16_gemm_bf16(w, x)
+    out = torch.zeros((T, rows), dtype=torch.int16, device=cuda)
+    if T == 1:
+        assert ops.k3_rocm_bf16_gemv_bf16(out, dev(w.view(np.int16), cuda),
+                                          dev(x.view(np.int16), cuda), rows, cols)
+    else:
+        assert ops.k3_rocm_bf16_gemm_bf16(out, dev(w.view(np.int16), cuda),
+                                          dev(x.view(np.int16), cuda), T, rows, cols)
+    sync()
+    np.testing.assert_array_equal(host(out).view(np.uint16), want)
+    for tile in (16, 32, 64):
+        o2 = torch.zeros_like(out)
+        assert ops.k3_rocm_bf16_gemm_tiled_bf16(o2, dev(w.view(np.int16), cuda),
+                                                dev(x.view(np.int16), cuda), T, rows, cols, tile)
+        sync()
+        assert torch.equal(o2, out)
+
+
+def test_q8_quantize_dequantize_bitexact(cuda):
+    rng = np.random.default_rng(21)
+    rows, cols = 300, 1024
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    w[3, 256:384] = 0.0
+    w[4, :128] = np.linspace(-3, 3, 128)
+    wb = f32_to_bf16_bits(w)
+    want_q, want_s = O.q8_quantize(wb)
+    q = torch.zeros((rows, cols), dtype=torch.int8, device=cuda)
+    s = torch.zeros((rows, cols // 128), dtype=torch.float32, device=cuda)
+    assert ops.k3_rocm_bf16_quantize_q8_128(q, s, dev(wb.view(np.int16), cuda), rows, cols)
+    sync()
+    np.testing.assert_array_equal(host(q), want_q)
+    np.testing.assert_array_equal(host(s), want_s)
+    d = torch.zeros((rows, cols), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_q8_128_dequantize_bf16(d, q, s, rows, cols)
+    sync()
+    np.testing.assert_array_equal(host(d).view(np.uint16), O.q8_dequantize(want_q, want_s))
+    # argument checks: columns % 128
+    assert not ops.k3_rocm_bf16_quantize_q8_128(q, s, dev(wb.view(np.int16), cuda), rows, 1000)
+
+
+@pytest.mark.parametrize("T,rows,cols", [(1, 3584, 7168), (1, 7168, 3584), (3, 96, 1024),
+                                         (17, 64, 6144), (64, 33, 2048)])
+def test_q8_gemm_bitexact(cuda, T, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols + T)
+    q = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+    s = (rng.random((rows, cols // 128)) * 1e-3 + 1e-4).astype(np.float32)
+    x = rand_bf16(rng, (T, cols))
+    want, _ = O.q8_gemm(q, s, x)
+    qd, sd, xd = dev(q, cuda), dev(s, cuda), dev(x.view(np.int16), cuda)
+    out = torch.zeros((T, rows), dtype=torch.int16, device=cuda)
+    if T == 1:
+        assert ops.k3_rocm_q8_128_gemv_bf16(out, qd, sd, xd, rows, cols)
+    else:
+        assert ops.k3_rocm_q8_128_gemm_bf16(out, qd, sd, xd, T, rows, cols)
+    sync()
+    np.testing.assert_array_equal(host(out).view(np.uint16), want)
+    for tile in (16, 32, 64):
+        o2 = torch.zeros_like(out)
+        assert ops.k3_rocm_q8_128_gemm_tiled_bf16(o2, qd, sd, xd, T, rows, cols, tile)
+        sync()
+        assert torch.equal(o2, out)
+    # codes at an 8-byte (not 16-byte) aligned address: the reference reads
+    # 8-byte octets, so such starts are accepted
+    buf = torch.zeros(rows * cols + 16, dtype=torch.int8, device=cuda)
+    buf[8:8 + rows * cols] = qd.view(-1)
+    o3 = torch.zeros_like(out)
+    assert ops.k3_rocm_q8_128_gemm_bf16(o3, buf[8:], sd, xd, T, rows, cols)
+    sync()
+    assert torch.equal(o3, out)
+
+
+@pytest.mark.parametrize("T,H", [(1, 3584), (5, 7168), (3, 100)])
+def test_rms_norm_bitexact(cuda, T, H):
+    rng = np.random.default_rng(T * H)
+    x = rand_bf16(rng, (T, H), 3.0)
+    w = f32_to_bf16_bits(rng.normal(1, 0.1, H).astype(np.float32))
+    want = O.rms_norm(x, w, 1e-5)
+    out = torch.zeros((T, H), dtype=torch.int16, device=cuda)
+    assert ops.k3_rocm_rms_norm_bf16(out, dev(x.view(np.int16), cuda), dev(w.view(np.int16), cuda),
+                                     T, H, 1e-5)
+    sync()
+    np.testing.assert_array_equal(host(out).view(np.uint16), want)

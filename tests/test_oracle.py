@@ -353,3 +353,94 @@ def test_split_layer_matches_fp64_layer():
     ye = bf16_bits_to_f32(ex["expert_out"]).astype(np.float64)
     ys = bf16_bits_to_f32(sp["expert_out"]).astype(np.float64)
     assert np.linalg.norm(ys - ye) / np.linalg.norm(ye) < 1e-4
+
+
+def _fmaf(a, b, c):
+    """fmaf(a, b, c) for operands whose product is exact in float64 and whose
+    sum with c is exact in float64 (true for the q8 KAT data below)."""
+    return np.float32(np.float64(a) * np.float64(b) + np.float64(c))
+
+
+def test_q8_quantize_vs_numpy_and_round_trip():
+    rng = np.random.default_rng(11)
+    w = rng.normal(0, 0.02, (6, 512)).astype(np.float32)
+    w[1, 128:256] = 0.0                      # all-zero block: scale 1, codes 0
+    w[2, :128] = np.linspace(-3, 3, 128)     # codes hit +-127 exactly
+    wb = f32_to_bf16_bits(w)
+    q, s = O.q8_quantize(wb)
+    wf = bf16_bits_to_f32(wb).reshape(6, 4, 128)
+    amax = np.abs(wf).max(axis=2)
+    want_s = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    np.testing.assert_array_equal(s, want_s)
+    want_q = np.clip(np.rint(wf / want_s[:, :, None]), -127, 127).astype(np.int8).reshape(6, 512)
+    np.testing.assert_array_equal(q, want_q)
+    assert s[1, 1] == 1.0 and (q[1, 128:256] == 0).all()
+    assert q[2, 0] == -127 and q[2, 127] == 127
+    # dequantize = bf16(q * scale); error within half a step (+ bf16 rounding)
+    d = O.q8_dequantize(q, s)
+    np.testing.assert_array_equal(
+        d, f32_to_bf16_bits(q.astype(np.float32) * np.repeat(s, 128, axis=1)))
+    err = np.abs(bf16_bits_to_f32(d) - bf16_bits_to_f32(wb)).reshape(6, 4, 128)
+    assert np.all(err <= s[:, :, None] * 0.5 + np.abs(wf) * 2.0 ** -8)
+
+
+def test_q8_gemm_order_brute_force_and_envelope():
+    rng = np.random.default_rng(12)
+    # brute force of the w64 order on power-of-two scales (every fmaf exact
+    # in float64): lane l owns 32-column groups l, l + 64, ...
+    rows, cols = 3, 4096 + 128
+    q = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+    s = np.ldexp(1.0, rng.integers(-12, -4, (rows, cols // 128))).astype(np.float32)
+    x = f32_to_bf16_bits(rng.normal(0, 1, (2, cols)).astype(np.float32))
+    got, f = O.q8_gemm(q, s, x)
+    xf = bf16_bits_to_f32(x)
+    for t in range(2):
+        for r in range(rows):
+            lanes = np.zeros(64, np.float32)
+            for lane in range(64):
+                acc = np.float32(0.0)
+                for g in range(lane, cols // 32, 64):
+                    gs = np.float32(0.0)
+                    for i in range(32 * g, 32 * g + 32):
+                        gs = _fmaf(np.float32(q[r, i]), xf[t, i], gs)
+                    acc = _fmaf(gs, s[r, g // 4], acc)
+                lanes[lane] = acc
+            for o in (32, 16, 8, 4, 2, 1):
+                lanes = (lanes + lanes[np.arange(64) ^ o]).astype(np.float32)
+            assert f[t, r] == lanes[0]
+    # fp64 envelope of the w64 and reference orders on real-sized rows
+    w = f32_to_bf16_bits(rng.normal(0, 0.02, (64, 7168)).astype(np.float32))
+    q, s = O.q8_quantize(w)
+    x = f32_to_bf16_bits(rng.normal(0, 1, (2, 7168)).astype(np.float32))
+    _, f64 = O.q8_gemm(q, s, x, O.ORDER_F64)
+    for order in (O.ORDER_W64, O.ORDER_REF):
+        got, f = O.q8_gemm(q, s, x, order)
+        assert np.all(np.abs(f - f64) <= 1e-5 * np.maximum(1, np.abs(f64)))
+        assert np.all(np.abs(bf16_bits_to_f32(got) - f64) <= np.abs(f64) * 2.0 ** -8 + 1e-6)
+    # single nonzero code: exact product
+    q = np.zeros((1, 256), np.int8)
+    s = np.array([[0.5, 4.0]], np.float32)
+    q[0, 200] = -3
+    x = np.zeros((1, 256), np.uint16)
+    x[0, 200] = f32_to_bf16_bits(np.array([2.5], np.float32))[0]
+    got, _ = O.q8_gemm(q, s, x)
+    assert bf16_bits_to_f32(got)[0, 0] == -30.0
+
+
+def test_rms_norm_closed_form_and_fp64():
+    # constant input c: rms = |c|, out = c / sqrt(c^2 + eps) * w
+    H = 3584
+    x = f32_to_bf16_bits(np.full((1, H), -2.0, np.float32))
+    w = f32_to_bf16_bits(np.linspace(0.5, 1.5, H).astype(np.float32))
+    got = bf16_bits_to_f32(O.rms_norm(x, w, 1e-5))
+    want = -2.0 / math.sqrt(4.0 + 1e-5) * bf16_bits_to_f32(w)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -8)
+    rng = np.random.default_rng(13)
+    for H in (3584, 7168, 100):
+        x = f32_to_bf16_bits(rng.normal(0, 3, (4, H)).astype(np.float32))
+        w = f32_to_bf16_bits(rng.normal(1, 0.1, H).astype(np.float32))
+        ours = bf16_bits_to_f32(O.rms_norm(x, w))
+        ref = bf16_bits_to_f32(O.rms_norm(x, w, order=O.ORDER_REF))
+        f64 = bf16_bits_to_f32(O.rms_norm(x, w, order=O.ORDER_F64))
+        for got in (ours, ref):  # within one bf16 rounding of the fp64 result
+            assert np.all(np.abs(got - f64) <= np.abs(f64) * 2.0 ** -8 + 1e-30)
