@@ -195,6 +195,69 @@ bool k3_moe_mx8_quantize_bf16(uint8_t *hi_codes, uint8_t *hi_scales, uint8_t *lo
                               void *stream);
 
 /*
+ * K3-native MoE layer: the routed experts run on a latent of width D (the
+ * `routed` shape's hidden) between two static projections, beside a dense
+ * shared expert (k3_engine.cu:1549-1563, 1668-1689, 1851-1897):
+ *
+ *   ids, w   = top-k(router(x))                      router on H columns
+ *   latent   = routed_down . x                       [D]
+ *   routed   = bf16(sum_r w_r * expert_r(latent))    rank order, no residual
+ *   full     = routed_up . rms_norm(routed, routed_norm, eps)     [H]
+ *   shared   = shared_down . act(shared_gate . x, shared_up . x)  [H]
+ *   output   = bf16(residual + bf16(full + shared))  (residual nullable)
+ *
+ * x is the post-attention-norm hidden state [T, H]; the shared expert uses
+ * the routed shape's activation. Static weights are bf16 or Q8-128
+ * (k3_static_store.h's two kinds). Each step is the library's own entry
+ * point of the same operation, so every intermediate is bit-identical to
+ * calling them in this order. No reference counterpart as one call: the
+ * reference engine issues these launches itself.
+ */
+typedef enum {
+    K3_MOE_STATIC_BF16 = 0,   /* data bf16 [rows, columns] */
+    K3_MOE_STATIC_Q8_128 = 1  /* data int8 [rows, columns], scales f32 [rows, columns / 128] */
+} k3_moe_static_kind;
+
+typedef struct {
+    uint32_t    kind;     /* k3_moe_static_kind */
+    uint32_t    rows;
+    uint32_t    columns;
+    const void *data;
+    const void *scales;   /* Q8-128 only */
+} k3_moe_static_weight;
+
+typedef struct {
+    k3_moe_shape routed;         /* hidden = latent D; experts, top-k, F, scale, activation */
+    uint32_t     model_hidden;   /* H: router columns, layer input/output width */
+    uint32_t     shared_hidden;  /* shared expert intermediate width */
+    float        norm_epsilon;   /* routed RMSNorm epsilon (1e-5 in K3) */
+} k3_moe_native_shape;
+
+typedef struct {
+    const void           *router_weight;  /* bf16 [E, H] */
+    const void           *router_bias;    /* f32 [E] */
+    k3_moe_static_weight  routed_down;    /* [D, H] */
+    const void           *routed_norm;    /* bf16 [D] */
+    k3_moe_static_weight  routed_up;      /* [H, D] */
+    k3_moe_static_weight  shared_gate;    /* [shared_hidden, H] */
+    k3_moe_static_weight  shared_up;      /* [shared_hidden, H] */
+    k3_moe_static_weight  shared_down;    /* [H, shared_hidden] */
+    const k3_moe_expert  *experts;        /* [E], on the latent */
+} k3_moe_native_weights;
+
+/* Bytes of workspace k3_moe_native_forward_bf16 needs for token_count rows. */
+size_t k3_moe_native_workspace_bytes(const k3_moe_native_shape *shape, uint32_t token_count);
+
+/* The layer above; expert_ids/expert_weights (nullable, [T, k]) receive
+ * the routes. output, x and residual rows 16-byte aligned; precision as
+ * for k3_moe_forward_bf16 (it selects the expert products' arithmetic). */
+bool k3_moe_native_forward_bf16(void *output, const void *hidden, const void *residual,
+                                const k3_moe_native_weights *weights,
+                                const k3_moe_native_shape *shape, uint32_t token_count,
+                                uint32_t precision, void *expert_ids, void *expert_weights,
+                                void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Synthetic resident expert store for benchmarks and tests: fills `bytes`
  * of device memory at `base` with the counter-based generator
  * k3_moe_synth_byte(seed, stream, index) below. Packed tensors use uniform

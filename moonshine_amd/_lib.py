@@ -45,6 +45,29 @@ class K3MoeExpert(ctypes.Structure):
     ]
 
 
+class K3MoeStaticWeight(ctypes.Structure):
+    """k3_moe_static_weight (include/k3_moe.h)."""
+
+    _fields_ = [("kind", _u32), ("rows", _u32), ("columns", _u32), ("data", _p),
+                ("scales", _p)]
+
+
+class K3MoeNativeShape(ctypes.Structure):
+    """k3_moe_native_shape (include/k3_moe.h)."""
+
+    _fields_ = [("routed", K3MoeShape), ("model_hidden", _u32), ("shared_hidden", _u32),
+                ("norm_epsilon", _f)]
+
+
+class K3MoeNativeWeights(ctypes.Structure):
+    """k3_moe_native_weights (include/k3_moe.h)."""
+
+    _fields_ = [("router_weight", _p), ("router_bias", _p), ("routed_down", K3MoeStaticWeight),
+                ("routed_norm", _p), ("routed_up", K3MoeStaticWeight),
+                ("shared_gate", K3MoeStaticWeight), ("shared_up", K3MoeStaticWeight),
+                ("shared_down", K3MoeStaticWeight), ("experts", _p)]
+
+
 STAGES = ("router", "topk", "plan", "gate_up", "down", "combine", "end")
 
 
@@ -81,6 +104,10 @@ SIGNATURES = {
     "k3_rocm_scatter_rows_bf16": (_b, [_p, _p, _p, _u32, _u32, _p]),
     "k3_rocm_add_bf16": (_b, [_p, _p, _p, _u64, _p]),
     "k3_moe_workspace_bytes": (_sz, [ctypes.POINTER(K3MoeShape), _u32]),
+    "k3_moe_native_workspace_bytes": (_sz, [ctypes.POINTER(K3MoeNativeShape), _u32]),
+    "k3_moe_native_forward_bf16": (_b, [_p, _p, _p, ctypes.POINTER(K3MoeNativeWeights),
+                                        ctypes.POINTER(K3MoeNativeShape), _u32, _u32, _p, _p,
+                                        _p, _sz, _p]),
     "k3_moe_workspace_init": (_b, [_p, _sz, _p]),
     "k3_moe_plan_scratch_bytes": (_sz, [_u32, _u32]),
     "k3_moe_route_plan": (_b, [_p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _p, _sz, _p]),

@@ -264,3 +264,34 @@ def layer(cfg, inputs, experts, tokens=None, ids=None, weights=None, order=ORDER
     if rc != 0:
         raise RuntimeError(f"k3o_layer failed ({rc})")
     return dict(output=out, ids=ids_out, weights=w_out, logits=logits, expert_out=yout)
+
+
+def native_layer(ncfg, router_weight, router_bias, norm, statics, x, residual, experts):
+    """K3-native MoE layer from the oracle's pieces, in the order of
+    k3_engine.cu:1549-1563, 1668-1689, 1851-1897 (include/k3_moe.h).
+    statics: name -> (kind, data, scales) with kind 0 = bf16 bits, 1 = Q8-128."""
+    from moonshine_amd.synth import Config, HostInputs
+    T = x.shape[0]
+
+    def proj(name, inp):
+        kind, data, scales = statics[name]
+        if kind == 0:
+            return bf16_gemm_bf16(data, inp)
+        return q8_gemm(data, scales, inp)[0]
+
+    logits = router_logits(router_weight, x)
+    ids, w = router_topk(logits, router_bias, ncfg.top_k, ncfg.scale)
+    latent = proj("routed_down", x)
+    rcfg = Config("routed", T, ncfg.latent, ncfg.experts, ncfg.top_k, ncfg.ffn, ncfg.scale,
+                  ncfg.activation, ncfg.beta, ncfg.linear_beta)
+    rin = HostInputs(np.zeros((ncfg.experts, ncfg.latent), np.uint16), router_bias, latent, None)
+    routed = layer(rcfg, rin, experts, ids=ids, weights=w)["output"]
+    normed = rms_norm(routed, norm, ncfg.eps)
+    full = proj("routed_up", normed)
+    g, u = proj("shared_gate", x), proj("shared_up", x)
+    a = swiglu(g, u) if ncfg.activation == 1 else situ(g, u, ncfg.beta, ncfg.linear_beta)
+    shared = proj("shared_down", a)
+    total = add(full, shared)
+    out = add(residual, total) if residual is not None else total
+    return dict(output=out, ids=ids, weights=w, latent=latent, routed=routed, normed=normed,
+                full=full, shared=shared)
