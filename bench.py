@@ -112,6 +112,97 @@ def cpu_baseline(cfg, inputs_cpu, store, budget_s, threads):
                       f"jobs; {dt:.1f} s (+{gen_s:.1f} s regenerating experts, untimed)"}
 
 
+def run_native(args):
+    """The K3-native layer (router, Q8-128 latent projection, experts on the
+    latent, RMSNorm, up projection, SiTU shared expert, adds) at T tokens."""
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from moonshine_amd import native as N
+    from moonshine_amd._lib import lib
+    from moonshine_amd.synth import f32_to_bf16_bits
+
+    cfg = N.K3_NATIVE_LAYER
+    T = args.tokens or cfg.tokens
+    R = args.rotate or (16 if T == 1 else 1)
+    log(f"bench: {cfg.name} T={T} building weights and resident expert store ...")
+    layer = N.NativeLayer(cfg, device="cuda")
+    rng = np.random.default_rng(cfg.seed + 1)
+    xs = torch.from_numpy(f32_to_bf16_bits(rng.normal(0, 1, (R, T, cfg.hidden)).astype(
+        np.float32)).view(np.int16)).cuda()
+    rs = torch.from_numpy(f32_to_bf16_bits(rng.normal(0, 1, (R, T, cfg.hidden)).astype(
+        np.float32)).view(np.int16)).cuda()
+    out = torch.empty((T, cfg.hidden), dtype=torch.int16, device="cuda")
+    ids = torch.zeros((T, cfg.top_k), dtype=torch.int32, device="cuda")
+    wts = torch.zeros((T, cfg.top_k), dtype=torch.float32, device="cuda")
+    ws = layer.workspace(T)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    argvs = [[P(out), P(xs[i]), P(rs[i]), ctypes.byref(layer.weights), ctypes.byref(layer.shape),
+              T, args.precision, P(ids), P(wts), P(ws), ws.numel(), stream] for i in range(R)]
+
+    def step(i):
+        if not lib().k3_moe_native_forward_bf16(*argvs[i % R]):
+            raise RuntimeError("k3_moe_native_forward_bf16 failed")
+
+    unique_per_batch = []
+    for i in range(max(args.warmup, R)):
+        step(i)
+        if i < R:
+            torch.cuda.synchronize()
+            unique_per_batch.append(int(np.unique(ids.cpu().numpy()).size))
+    torch.cuda.synchronize()
+    log(f"bench: timing {args.steps} steps ...")
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    unique = float(np.mean([unique_per_batch[i % R] for i in range(args.steps)]))
+    per_expert = 3 * (cfg.ffn * cfg.latent // 2 + cfg.ffn * cfg.latent // 32)
+    nbytes = (unique * per_expert + layer.static_bytes() + cfg.experts * cfg.hidden * 2 +
+              4 * cfg.experts + 2 * cfg.latent + 3 * T * cfg.hidden * 2 + T * cfg.top_k * 8)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "K3-native MoE layer tok/s (HBM GB/s)",
+        "value": T / (ms * 1e-3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 experts, q8-128 static projections, bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded; resident in HBM)",
+        "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden,
+                   "latent": cfg.latent, "experts": cfg.experts, "top_k": cfg.top_k,
+                   "ffn": cfg.ffn, "shared": cfg.shared, "activation": "situ",
+                   "scale": cfg.scale, "static": "q8_128",
+                   "precision": ["exact", "mx8", "mx8-1term"][args.precision],
+                   "unique_experts": unique, "distinct_batches": R},
+        "roofline": {"kernel": "whole layer (12 launches)", "bound": "hbm", "achieved": gbps,
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gbps / HBM_PEAK_GBPS,
+                     "traffic": None, "algorithmic_bytes": nbytes, "avg_ms": ms},
+    }
+    if not args.no_cpu_baseline and T == 1:
+        log("bench: CPU baseline (composed C oracle) ...")
+        sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+        import _oracle as O  # CPU baseline only
+        statics = {n: w.host() for n, w in layer.statics().items()}
+        x0 = xs[0].cpu().numpy().view(np.uint16)
+        r0 = rs[0].cpu().numpy().view(np.uint16)
+        logits = O.router_logits(layer.router_weight_bits, x0)
+        sel, _ = O.router_topk(logits, layer.router_bias, cfg.top_k, cfg.scale)
+        experts = {int(e): layer.store.host_expert(int(e)) for e in np.unique(sel)}
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        n, t0 = 0, time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < args.cpu_budget:
+            O.native_layer(cfg, layer.router_weight_bits, layer.router_bias, layer.norm_bits,
+                           statics, x0, r0, experts)
+            n += 1
+        dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {
+            "value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} run(s) of one {cfg.name} token through the composed C oracle "
+                      f"(OpenMP in the projections and experts); {dt:.1f} s"}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +217,9 @@ def main():
                          "T = 1, so consecutive steps route to different experts and no step "
                          "finds its weights in the 256 MB last-level cache; 1 for T > 1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--native", action="store_true",
+                    help="the K3-native layer (Q8-128 static projections around the routed "
+                         "experts, shared expert) instead of a BASELINE config")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB, --steps times (the known-size "
                          "kernel that scales FETCH_SIZE/WRITE_SIZE counter readings)")
@@ -145,6 +239,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": n, "launches": args.steps}), flush=True)
+        return
+
+    if args.native:
+        run_native(args)
         return
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
