@@ -250,12 +250,19 @@ size_t k3_moe_native_workspace_bytes(const k3_moe_native_shape *shape, uint32_t 
 
 /* The layer above; expert_ids/expert_weights (nullable, [T, k]) receive
  * the routes. output, x and residual rows 16-byte aligned; precision as
- * for k3_moe_forward_bf16 (it selects the expert products' arithmetic). */
+ * for k3_moe_forward_bf16 (it selects the expert products' arithmetic).
+ * shared_stream (nullable, like the reference engine's shared_stream,
+ * k3_engine.cu:1668-1689) takes the latent projection and the shared
+ * expert's gate/up while `stream` routes; the call joins it back with
+ * events before the shared down projection, so the result and its
+ * completion on `stream` are the same as without it. The fork/join events
+ * are created once per host thread and device (no device memory). */
 bool k3_moe_native_forward_bf16(void *output, const void *hidden, const void *residual,
                                 const k3_moe_native_weights *weights,
                                 const k3_moe_native_shape *shape, uint32_t token_count,
                                 uint32_t precision, void *expert_ids, void *expert_weights,
-                                void *workspace, size_t workspace_bytes, void *stream);
+                                void *workspace, size_t workspace_bytes, void *stream,
+                                void *shared_stream);
 
 /*
  * Synthetic resident expert store for benchmarks and tests: fills `bytes`

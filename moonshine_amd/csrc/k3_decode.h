@@ -12,6 +12,7 @@ struct DecodeParams {
     uint16_t *output;
     const uint16_t *residual;
     const uint16_t *hidden_in;
+    const uint16_t *router_in;  /* router input rows (the layer's hidden_in unless set) */
     const uint16_t *router_weight;
     const float *router_bias;
     const k3_moe_expert *experts;
@@ -27,6 +28,7 @@ struct DecodeParams {
     uint16_t *y;            /* [k, hidden] bf16 per-slot expert outputs */
     uint32_t *slot_mask;    /* bit s: slot s has an expert */
     uint32_t hidden, ffn, expert_count, top_k;
+    uint32_t router_cols;       /* router input width (hidden unless set) */
     float scale;
     uint32_t activation;
     float beta, linear_beta;
@@ -44,10 +46,25 @@ struct StageMarker {
 bool decode_supported(const k3_moe_shape &s);
 /* router, top-k, gate/up, down, combine */
 bool decode_launch(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
+/* router and top-k only (decode_launch's first half) */
+bool decode_launch_route(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
 /* gate/up, down, combine on routes in p.ids / p.weights (resolve: look the
  * expert descriptors up first, for routes that did not come from
  * decode_launch's top-k) */
 bool decode_launch_experts(const DecodeParams &p, hipStream_t stream, const StageMarker &mark,
                            bool resolve);
+
+/* One-token routed experts of the K3-native layer: router and top-k on x
+ * (router_cols wide), experts on `latent` (shape.hidden wide), output =
+ * bf16 rank-order combine with no residual. Uses the decode kernels; the
+ * workspace is the routed layer's (k3_moe_workspace_bytes(shape, 1)).
+ * With latent_ready, the experts wait for that event (the latent may be
+ * produced on another stream) while router and top-k do not. */
+bool native_decode_experts(void *routed_out, const void *x, uint32_t router_cols,
+                           const void *latent, const void *router_weight,
+                           const void *router_bias, const k3_moe_expert *experts,
+                           const k3_moe_shape &shape, void *ids_copy, void *w_copy,
+                           void *workspace, size_t workspace_bytes, hipEvent_t latent_ready,
+                           hipStream_t stream);
 
 }  // namespace k3

@@ -60,12 +60,12 @@ constexpr int kDownRows = 8;
  * so rereading x per row would cost as much as a third of the weights. */
 __global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
     const uint32_t lane = threadIdx.x;
-    const uint32_t chunks = P.hidden / 8u;
+    const uint32_t chunks = P.router_cols / 8u;
     const uint32_t row0 = 2u * blockIdx.x;
     const bool two = row0 + 1u < P.expert_count;
-    const uint4 *w0 = (const uint4 *)(P.router_weight + (uint64_t)row0 * P.hidden);
+    const uint4 *w0 = (const uint4 *)(P.router_weight + (uint64_t)row0 * P.router_cols);
     const uint4 *w1 = two ? w0 + chunks : w0;
-    const uint4 *x4 = (const uint4 *)P.hidden_in;
+    const uint4 *x4 = (const uint4 *)P.router_in;
     uint4 wa[kRouterMaxChunks], wb[kRouterMaxChunks], xv[kRouterMaxChunks];
 #pragma unroll
     for (int j = 0; j < kRouterMaxChunks; j++) {
@@ -407,12 +407,16 @@ bool decode_supported(const k3_moe_shape &s) {
            s.top_k <= 32u && s.expert_count <= 1024u;
 }
 
-bool decode_launch(const DecodeParams &P, hipStream_t st, const StageMarker &mark) {
+bool decode_launch_route(const DecodeParams &P, hipStream_t st, const StageMarker &mark) {
     mark(K3_MOE_STAGE_ROUTER);
     hipLaunchKernelGGL(router_kernel, dim3((P.expert_count + 1u) / 2u), dim3(64), 0, st, P);
     mark(K3_MOE_STAGE_TOPK);
     hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(64), 0, st, P);
-    return decode_launch_experts(P, st, mark, false);
+    return hipGetLastError() == hipSuccess;
+}
+
+bool decode_launch(const DecodeParams &P, hipStream_t st, const StageMarker &mark) {
+    return decode_launch_route(P, st, mark) && decode_launch_experts(P, st, mark, false);
 }
 
 bool decode_launch_experts(const DecodeParams &P, hipStream_t st, const StageMarker &mark,

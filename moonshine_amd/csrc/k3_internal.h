@@ -17,6 +17,18 @@ bool launch_bf16_rows_bf16_any(uint16_t *out, const void *weights, const void *i
                                uint32_t tokens, uint32_t rows, uint32_t cols,
                                hipStream_t stream);
 
+/* Single-vector Q8-128 projection for cols <= 8192 (bit-identical to the
+ * one-wave-per-row kernel); out = bf16(v), or bf16(add2 + bf16(add1 +
+ * bf16(v))) with the nullable addends. */
+bool q8_gemv_fits(uint32_t cols, const void *codes, const void *x);
+bool launch_q8_gemv(uint16_t *out, const void *codes, const void *scales, const void *x,
+                    uint32_t rows, uint32_t cols, const uint16_t *add1, const uint16_t *add2,
+                    hipStream_t stream);
+/* act = bf16(act(bf16(gate . x), bf16(up . x))) for two Q8-128 matrices. */
+bool launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gate_scales,
+                      const void *up_codes, const void *up_scales, const void *x, uint32_t rows,
+                      uint32_t cols, uint32_t kind, float beta, float lb, hipStream_t stream);
+
 /* Router top-k; ids2/w2 (nullable) receive extra copies (e.g. mapped host
  * memory) while ids/w stay in device memory for later kernels. */
 bool launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,

@@ -463,6 +463,8 @@ DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden
     P.output = (uint16_t *)output;
     P.residual = (const uint16_t *)residual;
     P.hidden_in = (const uint16_t *)hidden;
+    P.router_in = (const uint16_t *)hidden;
+    P.router_cols = s.hidden;
     P.router_weight = (const uint16_t *)router_weight;
     P.router_bias = (const float *)router_bias;
     P.experts = experts;
@@ -621,6 +623,27 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
         return false;
     return run_experts(ws, output, hidden, residual, experts, *shape, token_count, precision, st,
                        mark);
+}
+
+bool k3::native_decode_experts(void *routed_out, const void *x, uint32_t router_cols,
+                           const void *latent, const void *router_weight,
+                           const void *router_bias, const k3_moe_expert *experts,
+                           const k3_moe_shape &shape, void *ids_copy, void *w_copy,
+                           void *workspace, size_t workspace_bytes, hipEvent_t latent_ready,
+                           hipStream_t st) {
+    if (!decode_supported(shape) || router_cols == 0u || router_cols % 8u != 0u ||
+        router_cols > 8192u || (((uintptr_t)x | (uintptr_t)router_weight) % 16u) != 0u)
+        return false;
+    Workspace ws = carve(workspace, shape, 1u);
+    if (workspace_bytes < ws.bytes) return false;
+    DecodeParams P = decode_params(ws, routed_out, latent, nullptr, router_weight, router_bias,
+                                   experts, shape, ids_copy, w_copy);
+    P.router_in = (const uint16_t *)x;
+    P.router_cols = router_cols;
+    const StageMarker mark{nullptr, st};
+    if (!decode_launch_route(P, st, mark)) return false;
+    if (latent_ready && hipStreamWaitEvent(st, latent_ready, 0) != hipSuccess) return false;
+    return decode_launch_experts(P, st, mark, false);
 }
 
 extern "C" bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,

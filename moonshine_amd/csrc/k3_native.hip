@@ -7,6 +7,8 @@
  */
 #include "../../include/k3_moe.h"
 #include "../../include/k3_rocm_ops.h"
+#include "k3_decode.h"
+#include "k3_internal.h"
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -85,13 +87,42 @@ extern "C" size_t k3_moe_native_workspace_bytes(const k3_moe_native_shape *shape
     return carve(nullptr, *shape, token_count).bytes;
 }
 
+/* Fork/join events of the shared-stream form: created once per host thread
+ * and device (no device memory), reused by every call. A wait captures the
+ * event's latest record when it is enqueued, so re-recording for the next
+ * call cannot release an earlier wait. */
+namespace {
+
+struct StreamEvents {
+    int device = -1;
+    hipEvent_t fork = nullptr, latent = nullptr, act = nullptr;
+};
+
+bool stream_events(StreamEvents *&out) {
+    static thread_local StreamEvents cache[16];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return false;
+    StreamEvents &e = cache[dev];
+    if (e.device != dev) {
+        if (hipEventCreateWithFlags(&e.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&e.latent, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&e.act, hipEventDisableTiming) != hipSuccess)
+            return false;
+        e.device = dev;
+    }
+    out = &e;
+    return true;
+}
+
+}  // namespace
+
 extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, const void *residual,
                                            const k3_moe_native_weights *weights,
                                            const k3_moe_native_shape *shape,
                                            uint32_t token_count, uint32_t precision,
                                            void *expert_ids, void *expert_weights,
                                            void *workspace, size_t workspace_bytes,
-                                           void *stream) {
+                                           void *stream, void *shared_stream) {
     if (!output || !hidden || !weights || !workspace || !shape_ok(shape) || token_count == 0u ||
         token_count > 65535u)
         return false;
@@ -108,37 +139,88 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
     const NativeWorkspace ws = carve(workspace, s, T);
     if (workspace_bytes < ws.bytes || ((uintptr_t)workspace % kAlign) != 0u) return false;
     const hipStream_t st = (hipStream_t)stream;
-    const uint64_t n = (uint64_t)T * H;
-    /* router on the post-norm hidden state */
-    bool ok = k3_rocm_bf16_gemm_f32(ws.logits, W.router_weight, hidden, T, E, H, st) &&
-              k3_rocm_router_topk_f32_batch(ws.ids, ws.weights, ws.logits, W.router_bias, T, E,
-                                            k, s.routed.scaling_factor, st);
-    /* routed experts on the latent, combined in rank order */
-    ok = ok && project(W.routed_down, ws.latent, hidden, T, st) &&
-         k3_moe_experts_bf16(ws.routed, ws.latent, nullptr, ws.ids, ws.weights, W.experts,
-                             &s.routed, T, precision, ws.experts, ws.expert_bytes, st) &&
+    /* the side stream takes the latent projection and the shared expert's
+     * gate/up (both need only x); the main stream routes meanwhile */
+    StreamEvents *ev = nullptr;
+    const hipStream_t side = shared_stream && shared_stream != stream ? (hipStream_t)shared_stream
+                                                                      : st;
+    if (side != st && !stream_events(ev)) return false;
+    const float beta = s.routed.activation == K3_MOE_ACT_SWIGLU ? 1.0f : s.routed.beta;
+    const float lb = s.routed.activation == K3_MOE_ACT_SWIGLU ? 1.0f : s.routed.linear_beta;
+    const bool q8 = W.shared_gate.kind == K3_MOE_STATIC_Q8_128 &&
+                    W.shared_up.kind == K3_MOE_STATIC_Q8_128 &&
+                    W.shared_down.kind == K3_MOE_STATIC_Q8_128;
+    /* one token with Q8-128 weights: gate, up and the activation in one
+     * pass, and the down projection's epilogue forms bf16(residual +
+     * bf16(full + bf16(shared))) */
+    const bool fused = T == 1u && q8 && k3::q8_gemv_fits(H, W.shared_gate.data, hidden) &&
+                       k3::q8_gemv_fits(H, W.shared_up.data, hidden) &&
+                       k3::q8_gemv_fits(S, W.shared_down.data, ws.act);
+    const uint64_t sn = (uint64_t)T * S;
+    bool ok = true;
+    if (ev) {
+        ok = hipEventRecord(ev->fork, st) == hipSuccess &&
+             hipStreamWaitEvent(side, ev->fork, 0) == hipSuccess;
+    }
+    /* side stream (or the main one): latent, then the shared activation */
+    ok = ok && project(W.routed_down, ws.latent, hidden, T, side);
+    if (ev) ok = ok && hipEventRecord(ev->latent, side) == hipSuccess;
+    if (fused) {
+        ok = ok && k3::launch_q8_gateup(ws.act, W.shared_gate.data, W.shared_gate.scales,
+                                        W.shared_up.data, W.shared_up.scales, hidden, S, H,
+                                        s.routed.activation, beta, lb, side);
+    } else {
+        ok = ok && project(W.shared_gate, ws.gate, hidden, T, side) &&
+             project(W.shared_up, ws.up, hidden, T, side) &&
+             (s.routed.activation == K3_MOE_ACT_SWIGLU
+                  ? k3_rocm_swiglu_bf16(ws.act, ws.gate, ws.up, sn, side)
+                  : k3_rocm_situ_bf16(ws.act, ws.gate, ws.up, sn, s.routed.beta,
+                                      s.routed.linear_beta, side));
+    }
+    if (ev) ok = ok && hipEventRecord(ev->act, side) == hipSuccess;
+    /* main stream: routes, experts on the latent, norm, up projection */
+    const bool decode = T == 1u && k3::decode_supported(s.routed) && H % 8u == 0u &&
+                        H <= 8192u &&
+                        (((uintptr_t)hidden | (uintptr_t)W.router_weight) % 16u) == 0u;
+    bool routes_copied = false;
+    if (decode) {
+        ok = ok && k3::native_decode_experts(ws.routed, hidden, H, ws.latent, W.router_weight,
+                                             W.router_bias, W.experts, s.routed, expert_ids,
+                                             expert_weights, ws.experts, ws.expert_bytes,
+                                             ev ? ev->latent : nullptr, st);
+        routes_copied = true;
+    } else {
+        ok = ok && k3_rocm_bf16_gemm_f32(ws.logits, W.router_weight, hidden, T, E, H, st) &&
+             k3_rocm_router_topk_f32_batch(ws.ids, ws.weights, ws.logits, W.router_bias, T, E,
+                                           k, s.routed.scaling_factor, st) &&
+             (!ev || hipStreamWaitEvent(st, ev->latent, 0) == hipSuccess) &&
+             k3_moe_experts_bf16(ws.routed, ws.latent, nullptr, ws.ids, ws.weights, W.experts,
+                                 &s.routed, T, precision, ws.experts, ws.expert_bytes, st);
+    }
+    ok = ok &&
          k3_rocm_rms_norm_bf16(ws.normed, ws.routed, W.routed_norm, T, D, s.norm_epsilon, st) &&
          project(W.routed_up, ws.full, ws.normed, T, st);
-    /* shared expert */
-    const uint64_t sn = (uint64_t)T * S;
-    ok = ok && project(W.shared_gate, ws.gate, hidden, T, st) &&
-         project(W.shared_up, ws.up, hidden, T, st) &&
-         (s.routed.activation == K3_MOE_ACT_SWIGLU
-              ? k3_rocm_swiglu_bf16(ws.act, ws.gate, ws.up, sn, st)
-              : k3_rocm_situ_bf16(ws.act, ws.gate, ws.up, sn, s.routed.beta,
-                                  s.routed.linear_beta, st)) &&
-         project(W.shared_down, ws.shared, ws.act, T, st);
-    /* output = bf16(residual + bf16(full + shared)) */
-    if (residual)
-        ok = ok && k3_rocm_add_bf16(ws.sum, ws.full, ws.shared, n, st) &&
-             k3_rocm_add_bf16(output, residual, ws.sum, n, st);
-    else
-        ok = ok && k3_rocm_add_bf16(output, ws.full, ws.shared, n, st);
-    const size_t rb = (size_t)T * k * 4u;
-    if (ok && expert_ids)
-        ok = hipMemcpyAsync(expert_ids, ws.ids, rb, hipMemcpyDeviceToDevice, st) == hipSuccess;
-    if (ok && expert_weights)
-        ok = hipMemcpyAsync(expert_weights, ws.weights, rb, hipMemcpyDeviceToDevice, st) ==
-             hipSuccess;
+    if (ev) ok = ok && hipStreamWaitEvent(st, ev->act, 0) == hipSuccess;
+    if (fused) {
+        ok = ok && k3::launch_q8_gemv((uint16_t *)output, W.shared_down.data,
+                                      W.shared_down.scales, ws.act, H, S, ws.full,
+                                      (const uint16_t *)residual, st);
+    } else {
+        ok = ok && project(W.shared_down, ws.shared, ws.act, T, st);
+        const uint64_t n = (uint64_t)T * H;
+        if (residual) /* output = bf16(residual + bf16(full + shared)) */
+            ok = ok && k3_rocm_add_bf16(ws.sum, ws.full, ws.shared, n, st) &&
+                 k3_rocm_add_bf16(output, residual, ws.sum, n, st);
+        else
+            ok = ok && k3_rocm_add_bf16(output, ws.full, ws.shared, n, st);
+    }
+    if (!routes_copied) {
+        const size_t rb = (size_t)T * k * 4u;
+        if (ok && expert_ids)
+            ok = hipMemcpyAsync(expert_ids, ws.ids, rb, hipMemcpyDeviceToDevice, st) == hipSuccess;
+        if (ok && expert_weights)
+            ok = hipMemcpyAsync(expert_weights, ws.weights, rb, hipMemcpyDeviceToDevice, st) ==
+                 hipSuccess;
+    }
     return ok;
 }

@@ -420,6 +420,92 @@ bool launch_q8_rows(void *out, const void *q, const void *s, const void *x, uint
     return hipGetLastError() == hipSuccess;
 }
 
+/*
+ * Single-vector Q8-128 projections for cols <= 8192 (four 64-group K
+ * stripes, one per wave), R rows per block of 256 threads. Each lane loads
+ * its group of x once for all R rows; the unscaled group sums and their
+ * scales meet in LDS, and lane l then chains acc = fmaf(gs, scale, acc)
+ * over its groups l, l + 64, ... in order -- exactly q8_rows_kernel's per
+ * lane sequence -- before the same wave64 butterfly, so the outputs are
+ * bit-identical to it. One wave per row re-read x from L2 for every row,
+ * twice the bytes of the int8 weight row itself.
+ *
+ * DUAL: rows r of two matrices (gate, up) per block and out = bf16(act(
+ * bf16(gate), bf16(up))), the shared expert's gate/up/activation in one
+ * pass. Otherwise out = bf16(v), or with the epilogue addends
+ * bf16(add2 + bf16(add1 + bf16(v))) (two bf16 adds, in that order).
+ */
+constexpr int kQ8Rows = 8;
+
+template <bool DUAL>
+__global__ __launch_bounds__(256) void q8_gemv_kernel(
+        uint16_t *__restrict__ out, const int8_t *__restrict__ codes_a,
+        const float *__restrict__ scales_a, const int8_t *__restrict__ codes_b,
+        const float *__restrict__ scales_b, const uint16_t *__restrict__ x, uint32_t rows,
+        uint32_t cols, uint32_t align16, const uint16_t *__restrict__ add1,
+        const uint16_t *__restrict__ add2, uint32_t act_kind, float beta, float lb) {
+    constexpr int R = kQ8Rows, NM = DUAL ? 2 : 1;
+    __shared__ float part[NM * R][4][64];
+    __shared__ float scl[NM * R][4][64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t groups = cols / 32u, g = 64u * wave + lane;
+    if (g < groups) {
+        uint4 wa[NM * R], wb[NM * R];
+        float sc[NM * R];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const int8_t *q = m ? codes_b : codes_a;
+            const float *sp = m ? scales_b : scales_a;
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const uint32_t r = row0 + (uint32_t)i < rows ? row0 + (uint32_t)i : rows - 1u;
+                load_q8_group(q + (uint64_t)r * cols + 32u * g, align16, wa[m * R + i],
+                              wb[m * R + i]);
+                sc[m * R + i] = sp[(uint64_t)r * (cols / 128u) + (g >> 2)];
+            }
+        }
+        float xf[32];
+        bf16x32_to_f32((const uint4 *)x + 4u * g, xf);
+#pragma unroll
+        for (int i = 0; i < NM * R; i++) {
+            part[i][wave][lane] = q8_group(wa[i], wb[i], xf);
+            scl[i][wave][lane] = sc[i];
+        }
+    }
+    __syncthreads();
+    constexpr int RPW = R / 4; /* rows per wave in the reduction */
+    const uint32_t stripes = (groups + 63u) / 64u;
+    float p[NM * RPW];
+#pragma unroll
+    for (int q = 0; q < NM * RPW; q++) {
+        const int i = (q / RPW) * R + (int)wave * RPW + (q % RPW);
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < stripes; j++)
+            if (64u * j + lane < groups) acc = fmaf(part[i][j][lane], scl[i][j][lane], acc);
+        p[q] = acc;
+    }
+    const float v = wave_sum_rows<NM * RPW>(p);
+    if constexpr (DUAL) {
+        /* lanes < 32: gate rows, lanes >= 32: the same up rows */
+        const float u = __shfl_xor(v, 32, 64);
+        const float gb = bf16_to_f32(f32_to_bf16(v)), ub = bf16_to_f32(f32_to_bf16(u));
+        constexpr uint32_t kSpan = 32u / RPW;
+        const uint32_t row = row0 + RPW * wave + lane / kSpan;
+        if (lane < 32u && (lane & (kSpan - 1u)) == 0u && row < rows)
+            out[row] = f32_to_bf16(gated_act(gb, ub, act_kind, beta, lb));
+    } else {
+        const int owner = wave_rows_owner<RPW>();
+        const uint32_t row = row0 + RPW * wave + (uint32_t)owner;
+        if ((lane & (64u / RPW - 1u)) == 0u && row < rows) {
+            float r = bf16_to_f32(f32_to_bf16(v));
+            if (add1) r = bf16_to_f32(f32_to_bf16(__fadd_rn(bf16_to_f32(add1[row]), r)));
+            if (add2) r = __fadd_rn(bf16_to_f32(add2[row]), r);
+            out[row] = f32_to_bf16(r);
+        }
+    }
+}
+
 /* One wave per 128-element block: scale = max|w| / 127 (1 for an all-zero
  * block), code = clamp(rint(w / scale), -127, 127) with IEEE division;
  * a NaN weight codes as 0 (k3_rocm_ops.cu:662-697). */
@@ -502,23 +588,83 @@ __global__ void add_kernel(uint16_t *__restrict__ out, const uint16_t *__restric
         out[i] = f32_to_bf16(__fadd_rn(bf16_to_f32(a[i]), bf16_to_f32(b[i])));
 }
 
-__global__ void rms_norm_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ in,
-                                const uint16_t *__restrict__ weight, uint32_t hidden, float eps) {
+/* One block of 256 threads per vector. Order: thread t owns 8-element
+ * chunks t, t + 256, ... (elements in order within a chunk), s =
+ * fmaf(v, v, s); a wave64 butterfly per wave; total = (w0 + w1) + (w2 +
+ * w3); inv = 1 / sqrt(total / hidden + eps) (IEEE); out = bf16((x * inv) *
+ * weight). hidden <= 8192 with 16-byte rows keeps the vector in registers
+ * (every load issued up front: one memory round trip); otherwise the same
+ * order element by element. */
+constexpr int kRmsChunks = 4; /* 8-element chunks per thread: hidden <= 8192 */
+
+__global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t *__restrict__ out,
+                                                       const uint16_t *__restrict__ in,
+                                                       const uint16_t *__restrict__ weight,
+                                                       uint32_t hidden, float eps, uint32_t vec) {
     __shared__ float part[4];
+    const uint32_t t = threadIdx.x;
     const uint16_t *x = in + (uint64_t)blockIdx.x * hidden;
+    uint16_t *o = out + (uint64_t)blockIdx.x * hidden;
+    const uint32_t chunks = (hidden + 7u) / 8u;
     float s = 0.0f;
-    for (uint32_t d = threadIdx.x; d < hidden; d += blockDim.x) {
-        const float v = bf16_to_f32(x[d]);
-        s = fmaf(v, v, s);
+    if (vec) {
+        uint4 xv[kRmsChunks], wv[kRmsChunks];
+#pragma unroll
+        for (int j = 0; j < kRmsChunks; j++) {
+            const uint32_t c = t + 256u * (uint32_t)j;
+            if (c < chunks) {
+                xv[j] = ((const uint4 *)x)[c];
+                wv[j] = ((const uint4 *)weight)[c];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kRmsChunks; j++) {
+            if (t + 256u * (uint32_t)j < chunks) {
+                const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    s = fmaf(bf16_lo(u[q]), bf16_lo(u[q]), s);
+                    s = fmaf(bf16_hi(u[q]), bf16_hi(u[q]), s);
+                }
+            }
+        }
+        s = wave_sum(s);
+        if ((t & 63u) == 0u) part[t >> 6] = s;
+        __syncthreads();
+        const float total = __fadd_rn(__fadd_rn(part[0], part[1]), __fadd_rn(part[2], part[3]));
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)hidden), eps)));
+#pragma unroll
+        for (int j = 0; j < kRmsChunks; j++) {
+            const uint32_t c = t + 256u * (uint32_t)j;
+            if (c < chunks) {
+                const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+                const uint32_t w[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+                uint32_t r[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t lo = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_lo(u[q]), inv), bf16_lo(w[q])));
+                    const uint32_t hi = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_hi(u[q]), inv), bf16_hi(w[q])));
+                    r[q] = lo | (hi << 16);
+                }
+                ((uint4 *)o)[c] = make_uint4(r[0], r[1], r[2], r[3]);
+            }
+        }
+        return;
+    }
+    for (uint32_t c = t; c < chunks; c += 256u) {
+        const uint32_t end = 8u * c + 8u < hidden ? 8u * c + 8u : hidden;
+        for (uint32_t d = 8u * c; d < end; d++) {
+            const float v = bf16_to_f32(x[d]);
+            s = fmaf(v, v, s);
+        }
     }
     s = wave_sum(s);
-    if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = s;
+    if ((t & 63u) == 0u) part[t >> 6] = s;
     __syncthreads();
     const float total = __fadd_rn(__fadd_rn(part[0], part[1]), __fadd_rn(part[2], part[3]));
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)hidden), eps)));
-    for (uint32_t d = threadIdx.x; d < hidden; d += blockDim.x)
-        out[(uint64_t)blockIdx.x * hidden + d] =
-            f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(x[d]), inv), bf16_to_f32(weight[d])));
+    for (uint32_t d = t; d < hidden; d += 256u)
+        o[d] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(x[d]), inv), bf16_to_f32(weight[d])));
 }
 
 }  // namespace
@@ -734,9 +880,11 @@ extern "C" bool k3_rocm_rms_norm_bf16(void *output, const void *input, const voi
                                       uint32_t vector_count, uint32_t hidden_size, float epsilon,
                                       void *stream) {
     if (!output || !input || !weight || vector_count == 0u || hidden_size == 0u) return false;
+    const uint32_t vec = hidden_size % 8u == 0u && hidden_size <= 256u * 8u * kRmsChunks &&
+                         (((uintptr_t)output | (uintptr_t)input | (uintptr_t)weight) % 16u) == 0u;
     hipLaunchKernelGGL(rms_norm_kernel, dim3(vector_count), dim3(256), 0, (hipStream_t)stream,
                        (uint16_t *)output, (const uint16_t *)input, (const uint16_t *)weight,
-                       hidden_size, epsilon);
+                       hidden_size, epsilon, vec);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -830,8 +978,12 @@ extern "C" bool k3_rocm_q8_128_gemm_bf16(void *output, const void *quantized, co
                                          uint32_t columns, void *stream) {
     if (!q8_args_ok(output, quantized, scales, input, vector_count, rows, columns)) return false;
     const hipStream_t s = (hipStream_t)stream;
-    if (vector_count == 1u)
+    if (vector_count == 1u) {
+        if (k3::q8_gemv_fits(columns, quantized, input))
+            return k3::launch_q8_gemv((uint16_t *)output, quantized, scales, input, rows, columns,
+                                      nullptr, nullptr, s);
         return launch_q8_rows<1>(output, quantized, scales, input, 1u, rows, columns, s);
+    }
     if (vector_count <= 4u)
         return launch_q8_rows<4>(output, quantized, scales, input, vector_count, rows, columns, s);
     return launch_q8_rows<16>(output, quantized, scales, input, vector_count, rows, columns, s);
@@ -841,4 +993,35 @@ extern "C" bool k3_rocm_q8_128_gemv_bf16(void *output, const void *quantized, co
                                          const void *input, uint32_t rows, uint32_t columns,
                                          void *stream) {
     return k3_rocm_q8_128_gemm_bf16(output, quantized, scales, input, 1u, rows, columns, stream);
+}
+
+bool k3::q8_gemv_fits(uint32_t cols, const void *codes, const void *x) {
+    return cols != 0u && cols % 128u == 0u && cols <= 8192u && ((uintptr_t)codes % 8u) == 0u &&
+           ((uintptr_t)x % 16u) == 0u;
+}
+
+bool k3::launch_q8_gemv(uint16_t *out, const void *codes, const void *scales, const void *x,
+                        uint32_t rows, uint32_t cols, const uint16_t *add1, const uint16_t *add2,
+                        hipStream_t st) {
+    if (!q8_gemv_fits(cols, codes, x) || rows == 0u) return false;
+    const uint32_t align16 = ((uintptr_t)codes % 16u) == 0u;
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<false>), dim3((rows + kQ8Rows - 1u) / kQ8Rows),
+                       dim3(256), 0, st, out, (const int8_t *)codes, (const float *)scales,
+                       nullptr, nullptr, (const uint16_t *)x, rows, cols, align16, add1, add2, 0u,
+                       1.0f, 1.0f);
+    return hipGetLastError() == hipSuccess;
+}
+
+bool k3::launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gate_scales,
+                          const void *up_codes, const void *up_scales, const void *x,
+                          uint32_t rows, uint32_t cols, uint32_t kind, float beta, float lb,
+                          hipStream_t st) {
+    if (!q8_gemv_fits(cols, gate_codes, x) || !q8_gemv_fits(cols, up_codes, x) || rows == 0u)
+        return false;
+    const uint32_t align16 = (((uintptr_t)gate_codes | (uintptr_t)up_codes) % 16u) == 0u;
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<true>), dim3((rows + kQ8Rows - 1u) / kQ8Rows),
+                       dim3(256), 0, st, act, (const int8_t *)gate_codes, (const float *)gate_scales,
+                       (const int8_t *)up_codes, (const float *)up_scales, (const uint16_t *)x, rows,
+                       cols, align16, nullptr, nullptr, kind, beta, lb);
+    return hipGetLastError() == hipSuccess;
 }

@@ -134,7 +134,7 @@ class NativeLayer:
         return self._ws
 
     def forward(self, hidden, residual=None, out=None, ids=None, weights=None, precision=EXACT,
-                stream=None):
+                stream=None, shared_stream=None):
         T = hidden.shape[0]
         ws = self.workspace(T)
         if out is None:
@@ -144,7 +144,9 @@ class NativeLayer:
         ok = lib().k3_moe_native_forward_bf16(P(out), P(hidden), P(residual),
                                               ctypes.byref(self.weights), ctypes.byref(self.shape),
                                               T, precision, P(ids), P(weights), P(ws), ws.numel(),
-                                              ctypes.c_void_p(st))
+                                              ctypes.c_void_p(st),
+                                              None if shared_stream is None
+                                              else ctypes.c_void_p(shared_stream))
         if not ok:
             raise RuntimeError("k3_moe_native_forward_bf16 rejected its arguments or failed")
         return out

@@ -611,9 +611,17 @@ void k3o_rms_norm(uint16_t *out, const uint16_t *in, const uint16_t *weight,
         float p[256];
         for (uint32_t t = 0; t < 256u; t++) {
             float acc = 0.0f;
-            for (uint32_t d = t; d < hidden; d += 256u) {
-                const float e = k3o_bf16_to_f32(x[d]);
-                acc = order == 0 ? fmaf(e, e, acc) : acc + e * e;
+            if (order == 0) { /* 8-element chunks t, t + 256, ... */
+                for (uint32_t c = t; 8u * c < hidden; c += 256u)
+                    for (uint32_t d = 8u * c; d < 8u * c + 8u && d < hidden; d++) {
+                        const float e = k3o_bf16_to_f32(x[d]);
+                        acc = fmaf(e, e, acc);
+                    }
+            } else { /* reference: elements t, t + 256, ... */
+                for (uint32_t d = t; d < hidden; d += 256u) {
+                    const float e = k3o_bf16_to_f32(x[d]);
+                    acc = acc + e * e;
+                }
             }
             p[t] = acc;
         }

@@ -97,9 +97,9 @@ void k3o_q8_dequantize(uint16_t *w, const int8_t *q, const float *scales,
 void k3o_q8_gemm(uint16_t *out, float *out_f32, const int8_t *q,
                  const float *scales, const uint16_t *input, uint32_t vectors,
                  uint32_t rows, uint32_t cols, int order);
-/* order: 0 = the library's (256-thread strided fmaf, per-wave butterfly,
- * (w0 + w1) + (w2 + w3), IEEE 1/sqrt), 1 = reference 256-thread tree,
- * 2 = fp64 */
+/* order: 0 = the library's (thread t of 256 owns 8-element chunks t,
+ * t + 256, ... with fmaf(v, v, s); per-wave butterfly; (w0 + w1) + (w2 +
+ * w3); IEEE 1/sqrt), 1 = reference 256-thread tree, 2 = fp64 */
 void k3o_rms_norm(uint16_t *out, const uint16_t *in, const uint16_t *weight,
                   uint32_t vectors, uint32_t hidden, float eps, int order);
 

@@ -70,3 +70,29 @@ def test_native_mfma_close_to_exact(cuda):
     wf = (want["output"].astype(np.uint32) << 16).view(np.float32)
     rel = np.linalg.norm(gf - wf) / np.linalg.norm(wf)
     assert rel <= 2e-3, rel
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_native_shared_stream_same_bits(cuda, T):
+    """The shared-stream form (latent projection and shared gate/up on a
+    second stream, joined by events) gives the same bits, call after call."""
+    layer = N.NativeLayer(SMALL, device=cuda)
+    side = torch.cuda.Stream()
+    rng = np.random.default_rng(77 + T)
+    xs = [f32_to_bf16_bits(rng.normal(0, 1, (T, SMALL.hidden)).astype(np.float32)) for _ in range(2)]
+    rs = [f32_to_bf16_bits(rng.normal(0, 1, (T, SMALL.hidden)).astype(np.float32)) for _ in range(2)]
+    statics = host_statics(layer)
+    want = []
+    for x, r in zip(xs, rs):
+        ids = O.router_topk(O.router_logits(layer.router_weight_bits, x), layer.router_bias,
+                            SMALL.top_k, SMALL.scale)[0]
+        experts = {int(e): layer.store.host_expert(int(e)) for e in np.unique(ids)}
+        want.append(O.native_layer(SMALL, layer.router_weight_bits, layer.router_bias,
+                                   layer.norm_bits, statics, x, r, experts)["output"])
+    dx = [bf16_tensor(x, cuda) for x in xs]
+    dr = [bf16_tensor(r, cuda) for r in rs]
+    for rep in range(6):
+        i = rep % 2
+        out = layer.forward(dx[i], dr[i], shared_stream=side.cuda_stream)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bf16_bits(out), want[i])
