@@ -161,36 +161,46 @@ __global__ __launch_bounds__(64) void resolve_kernel(DecodeParams P) {
 /* gate/up                                                                 */
 /* ---------------------------------------------------------------------- */
 
+/* NS row sets of kGU gate and kGU up rows per block: NS = 2 when the
+ * input has at most two 64-group stripes (H <= 4096), so that all four
+ * waves load (two stripes x two sets) instead of two. */
+template <int NS>
 struct GateUpSmem {
-    float part[2 * kGU][4][64];
-    uint32_t scl[2 * kGU][64]; /* raw E8M0 bytes of row r, groups 0 .. G - 1 */
+    float part[NS][2 * kGU][4 / NS][64];
+    uint32_t scl[2 * NS * kGU][64]; /* raw E8M0 bytes: gate rows, then up rows */
 };
 
-/* grid (F / kGU, k), block 256; H <= 8192 (four 64-group stripes). */
+/* grid (F / (NS kGU), k), block 256; H <= 4096 NS (64-group stripes per
+ * set: 4 / NS). */
+template <int NS>
 __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
-    __shared__ GateUpSmem sm;
+    __shared__ GateUpSmem<NS> sm;
+    constexpr int SW = 4 / NS;    /* waves (stripes) per set */
+    constexpr int NR = NS * kGU;  /* gate rows per block */
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t slot = blockIdx.y, row0 = blockIdx.x * kGU;
+    const uint32_t set = wave / SW, stripe = wave % SW;
+    const uint32_t slot = blockIdx.y, row0 = blockIdx.x * NR;
     const uint32_t H = P.hidden, G = H / 32u;
     const k3_moe_expert ex = P.sel[slot];
     uint16_t *dst = P.act + (uint64_t)slot * P.ffn + row0;
     if (!ex.gate_packed) {
-        if (threadIdx.x < (uint32_t)kGU) dst[threadIdx.x] = 0;
+        if (threadIdx.x < (uint32_t)NR) dst[threadIdx.x] = 0;
         return;
     }
-    const uint32_t g = 64u * wave + lane;
+    const uint32_t g = 64u * stripe + lane;
     const uint8_t *gs = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G;
     const uint8_t *us = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G;
-    /* the block's scales are two contiguous runs of kGU G bytes (gate,
-     * up): fetched as whole lines of dwords, thread-contiguous, instead of
-     * a byte load per row and wave */
+    /* the block's scales are two contiguous runs of NR G bytes (gate, up):
+     * fetched as whole lines of dwords, thread-contiguous, instead of a
+     * byte load per row and wave */
     const bool words = G % 4u == 0u && (((uintptr_t)gs | (uintptr_t)us) & 3u) == 0u;
-    const uint32_t t = threadIdx.x, nd = kGU * G / 4u; /* dwords per run */
+    const uint32_t t = threadIdx.x, nd = NR * G / 4u; /* dwords per run */
+    const uint32_t srow0 = set * kGU; /* this wave's first row in the block */
     uint4 w[2 * kGU];
     uint32_t sw[4];
     if (g < G) {
-        const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u) + 16u * g;
-        const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u) + 16u * g;
+        const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)(row0 + srow0) * (H / 2u) + 16u * g;
+        const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)(row0 + srow0) * (H / 2u) + 16u * g;
 #pragma unroll
         for (int i = 0; i < kGU; i++) {
             w[i] = gload((const uint4 *)(gp + (uint64_t)i * (H / 2u)));
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
         float xf[32];
         bf16x32_to_f32((const uint4 *)P.hidden_in + 4u * g, xf);
 #pragma unroll
-        for (int r = 0; r < 2 * kGU; r++) sm.part[r][wave][lane] = fp4_group(w[r], xf);
+        for (int r = 0; r < 2 * kGU; r++) sm.part[set][r][stripe][lane] = fp4_group(w[r], xf);
     }
     uint8_t *sb = (uint8_t *)sm.scl;
     if (words) {
@@ -221,28 +231,32 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
             if (d < nd) { /* byte 4 d: row 4 d / G, group 4 d % G (G % 4 == 0) */
                 const uint32_t r = 4u * d / G, c4 = (4u * d % G) / 4u;
                 sm.scl[r][c4] = sw[k];
-                sm.scl[kGU + r][c4] = sw[2 + k];
+                sm.scl[NR + r][c4] = sw[2 + k];
             }
         }
     } else if (g < G) {
 #pragma unroll
-        for (int r = 0; r < 2 * kGU; r++)
-            sb[256u * (uint32_t)r + g] = (uint8_t)gload((r < kGU ? gs + (uint64_t)r * G
-                                                                 : us + (uint64_t)(r - kGU) * G) + g);
+        for (int i = 0; i < kGU; i++) {
+            const uint32_t r = srow0 + (uint32_t)i;
+            sb[256u * r + g] = (uint8_t)gload(gs + (uint64_t)r * G + g);
+            sb[256u * (NR + r) + g] = (uint8_t)gload(us + (uint64_t)r * G + g);
+        }
     }
     __syncthreads();
-    /* wave w: gate rows 2w, 2w+1 and the same up rows; lane l's groups
-     * l, l+64, ... in order */
-    constexpr int RPW = kGU / 4;
+    /* wave w: gate rows RPW w .. RPW w + RPW - 1 and the same up rows; lane
+     * l's groups l, l+64, ... in order */
+    constexpr int RPW = NR / 4;
     const uint32_t stripes = (G + 63u) / 64u;
     float p[2 * RPW];
 #pragma unroll
     for (int q = 0; q < 2 * RPW; q++) {
-        const int r = (q / RPW) * kGU + (int)wave * RPW + (q % RPW);
+        const uint32_t gr = RPW * wave + (uint32_t)(q % RPW); /* gate row in the block */
+        const uint32_t rs = gr / kGU, ri = gr % kGU + (q < RPW ? 0u : (uint32_t)kGU);
+        const uint32_t sr = q < RPW ? gr : NR + gr;
         float acc = 0.0f;
         for (uint32_t j = 0; j < stripes; j++)
             if (64u * j + lane < G)
-                acc = fmaf(sm.part[r][j][lane], e8m0_to_f32(sb[256u * (uint32_t)r + 64u * j + lane]), acc);
+                acc = fmaf(sm.part[rs][ri][j][lane], e8m0_to_f32(sb[256u * sr + 64u * j + lane]), acc);
         p[q] = acc;
     }
     const float v = wave_sum_rows<2 * RPW>(p); /* lanes < 32: gate, lanes >= 32: up */
@@ -298,11 +312,14 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
     /* issue order: the first weight stripe, then the block's activation
      * (one load per thread instead of one per wave) and the wave's scale
      * bytes (RB G contiguous bytes, dword loads when aligned) */
-    uint4 w[RB];
-    if (lane < G) {
+    uint4 w[M][RB]; /* every stripe's weights issued up front: one round trip */
 #pragma unroll
-        for (int i = 0; i < RB; i++)
-            w[i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * lane));
+    for (int m = 0; m < M; m++) {
+        if (lane + 64u * m < G) {
+#pragma unroll
+            for (int i = 0; i < RB; i++)
+                w[m][i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * (lane + 64u * m)));
+        }
     }
     uint4 xa[M];
 #pragma unroll
@@ -341,11 +358,6 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
     for (int m = 0; m < M; m++) {
         const uint32_t g = lane + 64u * m;
         if (g < G) {
-            if (m > 0) {
-#pragma unroll
-                for (int i = 0; i < RB; i++)
-                    w[i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g));
-            }
             uint4 xr[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) xr[q] = xs[q * 64 * M + g];
@@ -359,7 +371,7 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
                                      bf16_lo(xr[q].w), bf16_hi(xr[q].w)};
 #pragma unroll
                 for (int i = 0; i < RB; i++) {
-                    const uint32_t wq = q == 0 ? w[i].x : q == 1 ? w[i].y : q == 2 ? w[i].z : w[i].w;
+                    const uint32_t wq = q == 0 ? w[m][i].x : q == 1 ? w[m][i].y : q == 2 ? w[m][i].z : w[m][i].w;
                     gs[i] = fp4_dot8(wq, x8, gs[i]);
                 }
             }
@@ -424,7 +436,12 @@ bool decode_launch_experts(const DecodeParams &P, hipStream_t st, const StageMar
     mark(K3_MOE_STAGE_PLAN);
     if (resolve) hipLaunchKernelGGL(resolve_kernel, dim3(1), dim3(64), 0, st, P);
     mark(K3_MOE_STAGE_GATE_UP);
-    hipLaunchKernelGGL(gateup_kernel, dim3(P.ffn / kGU, P.top_k), dim3(256), 0, st, P);
+    if (P.hidden <= 4096u && P.ffn % (2u * kGU) == 0u)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_kernel<2>), dim3(P.ffn / (2u * kGU), P.top_k),
+                           dim3(256), 0, st, P);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_kernel<1>), dim3(P.ffn / kGU, P.top_k),
+                           dim3(256), 0, st, P);
     mark(K3_MOE_STAGE_DOWN);
     const dim3 block(256);
     if (P.ffn <= 2048u)
