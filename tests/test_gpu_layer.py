@@ -234,3 +234,68 @@ def test_route_plan_bitexact(cuda, T, E, k, zipf):
     np.testing.assert_array_equal(h(unique)[:u.size], u)
     np.testing.assert_array_equal(h(tok), t_i)
     np.testing.assert_array_equal(h(route), r_i)
+
+
+class MappedHost:
+    """hipHostMalloc'd, device-mapped host memory (the reference engine's
+    route outputs, k3_engine.cu:623-640); freed on close()."""
+
+    def __init__(self, nbytes):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t,
+                                           ctypes.c_uint]
+        self.hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p),
+                                                     ctypes.c_void_p, ctypes.c_uint]
+        self.hip.hipHostFree.argtypes = [ctypes.c_void_p]
+        self.host = ctypes.c_void_p()
+        assert self.hip.hipHostMalloc(ctypes.byref(self.host), nbytes, 0x2) == 0  # mapped
+        self.dev = ctypes.c_void_p()
+        assert self.hip.hipHostGetDevicePointer(ctypes.byref(self.dev), self.host, 0) == 0
+        self.nbytes = nbytes
+
+    def array(self, dtype, count):
+        buf = (ctypes.c_char * self.nbytes).from_address(self.host.value)
+        return np.frombuffer(buf, dtype=dtype, count=count)
+
+    def close(self):
+        self.hip.hipHostFree(self.host)
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_routes_into_mapped_host_memory(cuda, T):
+    """The layer's optional route copies written straight into host-mapped
+    memory, as the reference engine reads them."""
+    cfg = CONFIGS[0]
+    inputs = make_inputs(cfg, tokens=T, seed=cfg.seed + 9)
+    moe = get_layer(cfg, inputs, cuda)
+    n = T * cfg.top_k
+    mi, mw = MappedHost(4 * n), MappedHost(4 * n)
+    try:
+        mi.array(np.uint32, n)[:] = 0xDEADBEEF
+        mw.array(np.float32, n)[:] = -1.0
+        x = L.bf16_tensor(inputs.hidden, cuda)
+        r = L.bf16_tensor(inputs.residual, cuda)
+        ws = moe.workspace(T)
+        out = torch.empty_like(x)
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        assert lib().k3_moe_forward_bf16(P(out), P(x), P(r), P(moe.router_weight),
+                                         P(moe.router_bias), P(moe.store.table),
+                                         ctypes.byref(moe.shape), T, 0, mi.dev, mw.dev, P(ws),
+                                         ws.numel(),
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        want = O.layer(cfg, inputs, host_experts(moe.store, np.arange(cfg.experts)))
+        np.testing.assert_array_equal(mi.array(np.uint32, n).reshape(T, -1), want["ids"])
+        np.testing.assert_array_equal(mw.array(np.float32, n).reshape(T, -1), want["weights"])
+        np.testing.assert_array_equal(L.bf16_bits(out), want["output"])
+        # the single-vector router ABI into the same mapped buffers
+        from moonshine_amd import ops
+        logits = torch.from_numpy(O.router_logits(inputs.router_weight, inputs.hidden)[0]).to(cuda)
+        mi.array(np.uint32, n)[:] = 0
+        assert ops.lib().k3_rocm_router_topk_f32(mi.dev, mw.dev, P(logits), P(moe.router_bias),
+                                                 cfg.experts, cfg.top_k, cfg.scale, None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(mi.array(np.uint32, cfg.top_k), want["ids"][0])
+    finally:
+        mi.close()
+        mw.close()
