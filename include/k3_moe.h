@@ -30,9 +30,11 @@ extern "C" {
  * One routed expert in the checkpoint-native MXFP4 layout: packed
  * [rows, columns / 2] (low nibble = even column) and E8M0 scales
  * [rows, columns / 32]. Fields follow the six-tensor span order of
- * k3_prefill.c:71-75 (w1 = gate, w2 = down, w3 = up). Packed pointers must
- * be 16-byte aligned for the fused kernels, and scale pointers too for the
- * MXFP8 precisions (their kernels fetch scales 16 bytes per row at a time).
+ * k3_prefill.c:71-75 (w1 = gate, w2 = down, w3 = up). Tensors must start
+ * 8-byte aligned; the 8-mod-16 starts of real checkpoint spans
+ * (k3_rocm_ops.cu:207-223) are read as 8-byte pairs, and under the MXFP8
+ * precisions an expert with any tensor that is not 16-byte aligned runs on
+ * the exact kernels (the MFMA kernels stage 16-byte pieces).
  */
 typedef struct {
     const void *gate_packed;  /* w1.weight_packed [ffn, hidden / 2]  */

@@ -198,13 +198,15 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
     const uint32_t srow0 = set * kGU; /* this wave's first row in the block */
     uint4 w[2 * kGU];
     uint32_t sw[4];
+    /* 8-mod-16 tensor starts (real checkpoint spans) load as 8-byte pairs */
+    const bool a16 = (((uintptr_t)ex.gate_packed | (uintptr_t)ex.up_packed) % 16u) == 0u;
     if (g < G) {
         const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)(row0 + srow0) * (H / 2u) + 16u * g;
         const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)(row0 + srow0) * (H / 2u) + 16u * g;
 #pragma unroll
         for (int i = 0; i < kGU; i++) {
-            w[i] = gload((const uint4 *)(gp + (uint64_t)i * (H / 2u)));
-            w[kGU + i] = gload((const uint4 *)(up + (uint64_t)i * (H / 2u)));
+            w[i] = gload16(gp + (uint64_t)i * (H / 2u), a16);
+            w[kGU + i] = gload16(up + (uint64_t)i * (H / 2u), a16);
         }
     }
     if (words) {
@@ -313,12 +315,13 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
      * (one load per thread instead of one per wave) and the wave's scale
      * bytes (RB G contiguous bytes, dword loads when aligned) */
     uint4 w[M][RB]; /* every stripe's weights issued up front: one round trip */
+    const bool a16 = ((uintptr_t)ex.down_packed % 16u) == 0u;
 #pragma unroll
     for (int m = 0; m < M; m++) {
         if (lane + 64u * m < G) {
 #pragma unroll
             for (int i = 0; i < RB; i++)
-                w[m][i] = gload((const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * (lane + 64u * m)));
+                w[m][i] = gload16(dp + (uint64_t)i * (F / 2u) + 16u * (lane + 64u * m), a16);
         }
     }
     uint4 xa[M];

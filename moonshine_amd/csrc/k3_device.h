@@ -33,6 +33,14 @@ __device__ __forceinline__ uint4 gload(const uint4 *p) {
     const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+/* 16 packed bytes at p: one 16-byte load when p is 16-byte aligned, two
+ * 8-byte loads for the 8-mod-16 starts of real checkpoint spans
+ * (k3_rocm_ops.cu:207-223). a16 is block-uniform. */
+__device__ __forceinline__ uint4 gload16(const uint8_t *p, bool a16) {
+    if (a16) return gload((const uint4 *)p);
+    const uint2 lo = ((const uint2 *)p)[0], hi = ((const uint2 *)p)[1];
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
 __device__ __forceinline__ uint32_t gload(const uint8_t *p) {
     return *(const __attribute__((address_space(1))) uint8_t *)p;
 }

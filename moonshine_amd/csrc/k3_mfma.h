@@ -26,6 +26,8 @@ struct MfmaBuffers {
     uint8_t *aq[2], *as[2];     /* [routes, F] codes, [routes, F / 32] scales */
     uint32_t *tiles;            /* 3 classes x tile_cap x {expert, row0, rows} */
     uint32_t *tile_count;       /* [4] */
+    uint32_t *unaligned;        /* [E + 1]: count, then the selected experts with a
+                                   tensor that is not 16-byte aligned (any order) */
     uint32_t tile_cap[3];
 };
 

@@ -86,15 +86,30 @@ __global__ __launch_bounds__(256) void x_split_kernel(MfmaBuffers B, const uint1
 
 /* One block of 1024 threads (thread e = expert e). Class 0: experts with
  * <= 16 rows (one 16-row tile), class 1: <= 64 rows (one 64-row tile),
- * class 2: 128-row tiles. Tiles are listed in expert order. */
+ * class 2: 128-row tiles. Tiles are listed in expert order. An expert with
+ * a tensor that is not 16-byte aligned (the 8-mod-16 starts of real
+ * checkpoint spans) gets no tiles: direct-to-LDS loads move 16-byte
+ * pieces, so B.unaligned[e] hands it to the exact grouped kernels. */
 __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
                                                           const uint32_t *__restrict__ counts,
                                                           const uint32_t *__restrict__ offsets,
+                                                          const k3_moe_expert *__restrict__ experts,
                                                           uint32_t E) {
     __shared__ uint32_t wave_tot[3][16];
+    __shared__ uint32_t odd_count;
+    if (threadIdx.x == 0u) odd_count = 0u;
+    __syncthreads();
     const uint32_t e = threadIdx.x, lane = e & 63u, wave = e >> 6;
     const uint32_t n = e < E ? counts[e] : 0u;
-    const int cls = n == 0u ? 3 : (n <= 16u ? 0 : (n <= 64u ? 1 : 2));
+    bool odd = false;
+    if (n != 0u) {
+        const k3_moe_expert ex = experts[e];
+        odd = (((uintptr_t)ex.gate_packed | (uintptr_t)ex.gate_scales | (uintptr_t)ex.down_packed |
+                (uintptr_t)ex.down_scales | (uintptr_t)ex.up_packed | (uintptr_t)ex.up_scales) %
+               16u) != 0u;
+    }
+    if (odd) B.unaligned[1u + atomicAdd(&odd_count, 1u)] = e;
+    const int cls = n == 0u || odd ? 3 : (n <= 16u ? 0 : (n <= 64u ? 1 : 2));
     uint32_t nt[3], inc[3];
 #pragma unroll
     for (int c = 0; c < 3; c++) {
@@ -131,6 +146,7 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
         if (e == 0u) B.tile_count[c] = total;
         base_idx += B.tile_cap[c];
     }
+    if (e == 0u) B.unaligned[0] = odd_count; /* after the barrier above */
 }
 
 /* ---------------------------------------------------------------------- */
@@ -839,7 +855,7 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
     hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_kernel<TERMS>), dim3((uint32_t)((blocks + 255u) / 256u)),
                        dim3(256), 0, st, B, hidden, blocks);
     hipLaunchKernelGGL(tile_build_kernel, dim3(1), dim3(1024), 0, st, B, counts, offsets,
-                       s.expert_count);
+                       experts, s.expert_count);
     mark(K3_MOE_STAGE_GATE_UP);
     GateUpArgs ga{B, nullptr, nullptr, token_index, experts, H, F, s.activation,
                   s.activation == 1u ? 1.0f : s.beta, s.activation == 1u ? 1.0f : s.linear_beta};

@@ -104,6 +104,7 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
         mfma_tile_caps(T, s.top_k, s.expert_count, m.tile_cap);
         m.tiles = (uint32_t *)take(12ull * (m.tile_cap[0] + m.tile_cap[1] + m.tile_cap[2]));
         m.tile_count = (uint32_t *)take(16u);
+        m.unaligned = (uint32_t *)take(4ull * (s.expert_count + 1u));
     }
     w.bytes = off;
     return w;
@@ -248,18 +249,27 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
         const uint32_t *__restrict__ unique, const uint32_t *__restrict__ summary,
         const uint32_t *__restrict__ counts, const uint32_t *__restrict__ offsets,
         const uint32_t *__restrict__ token_index, const k3_moe_expert *__restrict__ experts,
-        uint32_t H, uint32_t F, uint32_t kind, float beta, float lb) {
-    const uint32_t u = blockIdx.y;
-    if (u >= summary[0]) return;
+        uint32_t H, uint32_t F, uint32_t kind, float beta, float lb, const uint32_t *list) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
     if (row0 >= F) return;
-    const uint32_t e = unique[u];
+    /* blockIdx.y indexes the selected experts, or with `list` (count, ids)
+     * walks that list with stride gridDim.y */
+    for (uint32_t q = blockIdx.y;; q += gridDim.y) {
+    uint32_t e;
+    if (list) {
+        if (q >= list[0]) return;
+        e = list[1u + q];
+    } else {
+        if (q != blockIdx.y || q >= summary[0]) return;
+        e = unique[q];
+    }
     const uint32_t n = counts[e], base = offsets[e];
     const k3_moe_expert ex = experts[e];
     const uint32_t G = H / 32u;
     const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u);
     const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u);
+    const bool a16 = (((uintptr_t)gp | (uintptr_t)up) % 16u) == 0u;
     const uint8_t *gsc = (const uint8_t *)ex.gate_scales + (uint64_t)row0 * G;
     const uint8_t *usc = (const uint8_t *)ex.up_scales + (uint64_t)row0 * G;
     for (uint32_t p0 = 0; p0 < n; p0 += TT) {
@@ -278,8 +288,8 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
             float sc[2 * RW];
 #pragma unroll
             for (int i = 0; i < RW; i++) {
-                w[i] = *(const uint4 *)(gp + (uint64_t)i * (H / 2u) + 16u * g);
-                w[RW + i] = *(const uint4 *)(up + (uint64_t)i * (H / 2u) + 16u * g);
+                w[i] = gload16(gp + (uint64_t)i * (H / 2u) + 16u * g, a16);
+                w[RW + i] = gload16(up + (uint64_t)i * (H / 2u) + 16u * g, a16);
                 sc[i] = e8m0_to_f32(gsc[(uint64_t)i * G + g]);
                 sc[RW + i] = e8m0_to_f32(usc[(uint64_t)i * G + g]);
             }
@@ -304,6 +314,7 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
                     f32_to_bf16(gated_act(bf16_round(v), bf16_round(uu), kind, beta, lb));
         }
     }
+    }
 }
 
 /* grid (H / (4 * RB), E_upper), block 256: y[route] = down_e . act[row]. */
@@ -313,17 +324,24 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
         const uint32_t *__restrict__ unique, const uint32_t *__restrict__ summary,
         const uint32_t *__restrict__ counts, const uint32_t *__restrict__ offsets,
         const uint32_t *__restrict__ route_index, const k3_moe_expert *__restrict__ experts,
-        uint32_t H, uint32_t F) {
-    const uint32_t u = blockIdx.y;
-    if (u >= summary[0]) return;
+        uint32_t H, uint32_t F, const uint32_t *list) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RB;
     if (row0 >= H) return;
-    const uint32_t e = unique[u];
+    for (uint32_t q = blockIdx.y;; q += gridDim.y) { /* as grouped_gateup_kernel */
+    uint32_t e;
+    if (list) {
+        if (q >= list[0]) return;
+        e = list[1u + q];
+    } else {
+        if (q != blockIdx.y || q >= summary[0]) return;
+        e = unique[q];
+    }
     const uint32_t n = counts[e], base = offsets[e];
     const k3_moe_expert ex = experts[e];
     const uint32_t G = F / 32u;
     const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
+    const bool a16 = ((uintptr_t)dp % 16u) == 0u;
     const uint8_t *ds = (const uint8_t *)ex.down_scales + (uint64_t)row0 * G;
     for (uint32_t p0 = 0; p0 < n; p0 += TT) {
         const uint32_t active = n - p0 < (uint32_t)TT ? n - p0 : (uint32_t)TT;
@@ -337,7 +355,7 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
             float sc[RB];
 #pragma unroll
             for (int i = 0; i < RB; i++) {
-                w[i] = *(const uint4 *)(dp + (uint64_t)i * (F / 2u) + 16u * g);
+                w[i] = gload16(dp + (uint64_t)i * (F / 2u) + 16u * g, a16);
                 sc[i] = e8m0_to_f32(ds[(uint64_t)i * G + g]);
             }
 #pragma unroll
@@ -358,6 +376,7 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
             if ((uint32_t)t < active && (lane & (64u / RB - 1u)) == 0u)
                 y[(uint64_t)route_index[base + p0 + t] * H + row0 + owner] = f32_to_bf16(v);
         }
+    }
     }
 }
 
@@ -490,6 +509,11 @@ DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden
     return P;
 }
 
+/* Experts the MFMA path hands to the exact kernels (tensors not 16-byte
+ * aligned) are walked by a grid of this many expert rows: with none, the
+ * blocks exit at once. */
+constexpr uint32_t kFallbackExperts = 8;
+
 /* Expert stage on routes already in ws.ids / ws.weights. */
 bool run_experts(const Workspace &ws, void *output, const void *hidden, const void *residual,
                  const k3_moe_expert *experts, const k3_moe_shape &s, uint32_t T,
@@ -506,11 +530,26 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
     if (!launch_plan(ws.counts, ws.offsets, ws.unique, ws.summary, ws.token_index,
                      ws.route_index, ws.chunk_base, ws.ids, T, k, E, st))
         return false;
+    const uint32_t upper = (uint64_t)T * k < E ? T * k : E;
+    constexpr int RW = 4, TT = 4, RB = 4;
     if (precision != K3_MOE_EXACT) {
         if (!mfma_launch_experts(ws.mfma, ws.y, (const uint16_t *)hidden, ws.counts, ws.offsets,
                                  ws.token_index, ws.route_index, experts, s, T,
                                  precision == K3_MOE_MFMA ? 2u : 1u, st, mark))
             return false;
+        /* experts with a tensor that is not 16-byte aligned (no MFMA tiles):
+         * the exact kernels, after the MFMA down kernel has consumed the
+         * activation codes that share `act` */
+        const uint32_t walk = upper < kFallbackExperts ? upper : kFallbackExperts;
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_gateup_kernel<RW, TT>),
+                           dim3(F / (4u * RW), walk), dim3(256), 0, st, ws.act,
+                           (const uint16_t *)hidden, ws.unique, ws.summary, ws.counts, ws.offsets,
+                           ws.token_index, experts, H, F, s.activation, beta, lb,
+                           (const uint32_t *)ws.mfma.unaligned);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TT>), dim3(H / (4u * RB), walk),
+                           dim3(256), 0, st, ws.y, ws.act, ws.unique, ws.summary, ws.counts,
+                           ws.offsets, ws.route_index, experts, H, F,
+                           (const uint32_t *)ws.mfma.unaligned);
         mark(K3_MOE_STAGE_COMBINE);
         hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
                            dim3(kCombineThreads), 0, st, (uint16_t *)output, ws.y,
@@ -518,17 +557,15 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
         mark(K3_MOE_STAGE_END);
         return hipGetLastError() == hipSuccess;
     }
-    const uint32_t upper = (uint64_t)T * k < E ? T * k : E;
-    constexpr int RW = 4, TT = 4, RB = 4;
     mark(K3_MOE_STAGE_GATE_UP);
     hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_gateup_kernel<RW, TT>), dim3(F / (4u * RW), upper),
                        dim3(256), 0, st, ws.act, (const uint16_t *)hidden, ws.unique, ws.summary,
                        ws.counts, ws.offsets, ws.token_index, experts, H, F, s.activation, beta,
-                       lb);
+                       lb, nullptr);
     mark(K3_MOE_STAGE_DOWN);
     hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TT>), dim3(H / (4u * RB), upper),
                        dim3(256), 0, st, ws.y, ws.act, ws.unique, ws.summary, ws.counts,
-                       ws.offsets, ws.route_index, experts, H, F);
+                       ws.offsets, ws.route_index, experts, H, F, nullptr);
     mark(K3_MOE_STAGE_COMBINE);
     hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
                        dim3(kCombineThreads), 0, st, (uint16_t *)output, ws.y,

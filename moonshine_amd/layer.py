@@ -37,23 +37,29 @@ class ExpertStore:
     E8M0 exponents 121..125.
     """
 
-    def __init__(self, experts, hidden, ffn, seed, device="cuda"):
+    def __init__(self, experts, hidden, ffn, seed, device="cuda", misalign=0, misalign_odd=False):
+        """misalign (0 or 8): start every tensor 8 bytes past a 16-byte
+        boundary, as real checkpoint spans do (k3_rocm_ops.cu:207-223);
+        misalign_odd: only the tensors of odd experts."""
         self.experts, self.hidden, self.ffn, self.seed = experts, hidden, ffn, seed
         self.sizes = expert_tensor_sizes(hidden, ffn)
         self.offsets = []
         off = 0
         for s in self.sizes:
             self.offsets.append(off)
-            off += _align(s)
+            off += _align(s + misalign)
         self.span = off
         self.payload_bytes = sum(self.sizes)
         self.buffer = torch.empty(experts * self.span, dtype=torch.uint8, device=device)
         base = self.buffer.data_ptr()
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         table = np.zeros((experts, 6), dtype=np.uint64)
+        self.shifts = []
         for e in range(experts):
+            shift = misalign if (not misalign_odd or e % 2 == 1) else 0
+            self.shifts.append(shift)
             for j, (o, s) in enumerate(zip(self.offsets, self.sizes)):
-                ptr = base + e * self.span + o
+                ptr = base + e * self.span + o + shift
                 table[e, j] = ptr
                 if not lib().k3_moe_synth_fill(ctypes.c_void_p(ptr), s, seed, e * 8 + j, j & 1,
                                                stream):
@@ -72,7 +78,7 @@ class ExpertStore:
 
     def device_expert(self, e):
         """Views of expert e's six tensors in the device buffer."""
-        b = e * self.span
+        b = e * self.span + self.shifts[e]
         return [self.buffer[b + o: b + o + s] for o, s in zip(self.offsets, self.sizes)]
 
 
