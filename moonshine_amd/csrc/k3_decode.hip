@@ -8,18 +8,21 @@
  *                   the k selected expert descriptors once (their loads
  *                   start before ranking), so the expert kernels reach
  *                   their weights through a single load.
- *   gateup_kernel   one block per (slot, 8 F-rows): each of its four waves
- *                   streams one 64-group K-stripe of the 8 gate and 8 up
- *                   rows (a coalesced 1 KB row-stripe per load), group sums
- *                   meet in LDS and are combined in the w64 lane order, then
- *                   the activation. 4096 blocks keep ~64 MB of loads in
- *                   flight.
+ *   gateup_kernel   one block per (slot, 8 F-rows; 16 in two sets when
+ *                   H <= 4096): each wave streams one 64-group K-stripe of
+ *                   8 gate and 8 up rows (a coalesced 1 KB row-stripe per
+ *                   load), group sums meet in LDS and are combined in the
+ *                   w64 lane order, then the activation. 4096 blocks at
+ *                   the K3 shape keep ~64 MB of loads in flight.
  *   down_kernel     one block per (slot, 4 x 8 rows): each wave streams a
  *                   contiguous 8-row stripe of the slot's down matrix
  *                   (8 KB in flight per wave) against the activation
  *                   staged once per block in LDS, and writes bf16 y[slot].
  *   combine_kernel  rank-order weighted sum of the k slot rows plus the
  *                   residual.
+ *
+ * A K3-native layer runs the same kernels with the router reading the
+ * model's hidden state (router_in, router_cols) and the experts the latent.
  *
  * Every hand-off is a kernel boundary, so all loads and stores are plain
  * (cached). Fusing the stages into one launch was measured and dropped on
@@ -418,7 +421,8 @@ __global__ __launch_bounds__(256) void combine_kernel(DecodeParams P) {
 }  // namespace
 
 bool decode_supported(const k3_moe_shape &s) {
-    return s.hidden % (s.ffn <= 2048u ? 64u : 32u) == 0u && s.hidden <= 8192u && s.ffn % 32u == 0u && s.ffn <= 4096u &&
+    /* down grids: H / 32 blocks (F <= 2048) or H / 16 (F <= 4096) */
+    return s.hidden % 32u == 0u && s.hidden <= 8192u && s.ffn % 32u == 0u && s.ffn <= 4096u &&
            s.top_k <= 32u && s.expert_count <= 1024u;
 }
 

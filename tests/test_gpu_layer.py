@@ -91,9 +91,12 @@ def test_synth_store_host_matches_device(cuda):
 # multiple of the larger kernels' row tiles (6208 = 97 x 64), and top_k > 16
 DECODE_RAGGED = Config("decode-ragged-rows", 1, 6208, 128, 8, 1024, seed=1006)
 DECODE_TOPK20 = Config("decode-topk20", 1, 2048, 128, 20, 512, seed=1007)
+# hidden = 33 x 32: odd group count (byte-wise scale loads in gate/up)
+DECODE_ODD_GROUPS = Config("decode-odd-groups", 1, 1056, 64, 4, 512, seed=1008)
 
 
-@pytest.mark.parametrize("cfg", [CONFIGS[0], CONFIGS[1], K3_NATIVE, DECODE_RAGGED, DECODE_TOPK20],
+@pytest.mark.parametrize("cfg", [CONFIGS[0], CONFIGS[1], K3_NATIVE, DECODE_RAGGED, DECODE_TOPK20,
+                                 DECODE_ODD_GROUPS],
                          ids=lambda c: c.name)
 def test_decode_layer_bitexact(cuda, cfg):
     inputs = make_inputs(cfg)
