@@ -11,7 +11,9 @@ Prints one JSON line. `value` is layer tokens/s (wall clock over exactly
 --steps steps, synchronised on both sides). `roofline` is for the dominant
 kernel (decode gate/up for T = 1, timed live with HIP events recorded
 around its stage); `cpu_baseline` is the C oracle of the same layer timed
-on this host's cores on a bounded token sample.
+on this host's cores on a bounded token sample. For one token, `graph`
+adds the same steps replayed from a HIP graph (a serving loop's form; no
+host launch cost between kernels) -- reported beside `value`, not as it.
 """
 import argparse
 import ctypes
@@ -52,6 +54,32 @@ class Hip:
         f = ctypes.c_float()
         assert self.h.hipEventElapsedTime(ctypes.byref(f), a, b) == 0
         return f.value
+
+
+def graph_ms_per_step(torch, call, R, steps):
+    """The same steps replayed from a HIP graph: R consecutive calls (one per
+    input rotation) captured once on a side stream, replayed ceil(steps / R)
+    times, wall clock per step. call(i, stream_handle) enqueues step i."""
+    s = torch.cuda.Stream()  # default priority
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        call(0, s.cuda_stream)
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(R):
+                call(i, s.cuda_stream)
+    torch.cuda.synchronize()
+    reps = max(1, -(-steps // R))
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / (reps * R) * 1e3
+    del g
+    return ms
 
 
 def algorithmic_bytes(cfg, T, unique):
@@ -135,17 +163,19 @@ def run_native(args):
     ids = torch.zeros((T, cfg.top_k), dtype=torch.int32, device="cuda")
     wts = torch.zeros((T, cfg.top_k), dtype=torch.float32, device="cuda")
     ws = layer.workspace(T)
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    stream = torch.cuda.current_stream().cuda_stream
     side = torch.cuda.Stream()  # default priority, like every stream here
-    shared = ctypes.c_void_p(side.cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     argvs = [[P(out), P(xs[i]), P(rs[i]), ctypes.byref(layer.weights), ctypes.byref(layer.shape),
-              T, args.precision, P(ids), P(wts), P(ws), ws.numel(), stream, shared]
-             for i in range(R)]
+              T, args.precision, P(ids), P(wts), P(ws), ws.numel()] for i in range(R)]
+
+    def call(i, st, streams):
+        shared = ctypes.c_void_p(side.cuda_stream) if streams == 2 else None
+        if not lib().k3_moe_native_forward_bf16(*argvs[i % R], ctypes.c_void_p(st), shared):
+            raise RuntimeError("k3_moe_native_forward_bf16 failed")
 
     def step(i):
-        if not lib().k3_moe_native_forward_bf16(*argvs[i % R]):
-            raise RuntimeError("k3_moe_native_forward_bf16 failed")
+        call(i, stream, args.streams)
 
     unique_per_batch = []
     for i in range(max(args.warmup, R)):
@@ -175,13 +205,18 @@ def run_native(args):
         "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden,
                    "latent": cfg.latent, "experts": cfg.experts, "top_k": cfg.top_k,
                    "ffn": cfg.ffn, "shared": cfg.shared, "activation": "situ",
-                   "scale": cfg.scale, "static": "q8_128", "streams": 2,
+                   "scale": cfg.scale, "static": "q8_128", "streams": args.streams,
                    "precision": ["exact", "mx8", "mx8-1term"][args.precision],
                    "unique_experts": unique, "distinct_batches": R},
         "roofline": {"kernel": "whole layer", "bound": "hbm", "achieved": gbps,
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gbps / HBM_PEAK_GBPS,
                      "traffic": None, "algorithmic_bytes": nbytes, "avg_ms": ms},
     }
+    if not args.no_graph:
+        log("bench: the same steps replayed from a HIP graph (two streams) ...")
+        gms = graph_ms_per_step(torch, lambda i, st: call(i, st, 2), R, args.steps)
+        result["graph"] = {"streams": 2, "ms_per_step": gms, "value": T / (gms * 1e-3),
+                           "hbm_gbps": nbytes / (gms * 1e-3) / 1e9}
     if not args.no_cpu_baseline and T == 1:
         log("bench: CPU baseline (composed C oracle) ...")
         sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
@@ -223,6 +258,11 @@ def main():
     ap.add_argument("--native", action="store_true",
                     help="the K3-native layer (Q8-128 static projections around the routed "
                          "experts, shared expert) instead of a BASELINE config")
+    ap.add_argument("--streams", type=int, default=1, choices=(1, 2),
+                    help="--native: 2 runs the latent projection and the shared expert's gate/up "
+                         "on a second stream (host-bound when not in a graph)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the extra HIP-graph replay figure (`graph` in the JSON line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB, --steps times (the known-size "
                          "kernel that scales FETCH_SIZE/WRITE_SIZE counter readings)")
@@ -306,6 +346,16 @@ def main():
         step(i, ctypes.byref(profiles[i]))
     torch.cuda.synchronize()
 
+    graph = None
+    if not args.no_graph and T == 1:
+        log("bench: the same steps replayed from a HIP graph ...")
+
+        def gcall(i, st):
+            if not lib().k3_moe_forward_profiled_bf16(*argvs[i % R], None, ctypes.c_void_p(st)):
+                raise RuntimeError("k3_moe_forward_profiled_bf16 failed")
+        gms = graph_ms_per_step(torch, gcall, R, args.steps)
+        graph = {"ms_per_step": gms, "value": T / (gms * 1e-3)}
+
     stage_ms = {s: 0.0 for s in STAGES[:-1]}
     gpu_ms = 0.0
     for p in profiles:
@@ -364,6 +414,8 @@ def main():
                   "gpu_ms_events": gpu_ms, "stage_ms": stage_ms},
         "roofline": roofline,
     }
+    if graph:
+        result["graph"] = graph
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (C oracle) ...")
         threads = min(len(os.sched_getaffinity(0)), 16)

@@ -255,10 +255,13 @@ size_t k3_moe_native_workspace_bytes(const k3_moe_native_shape *shape, uint32_t 
  * for k3_moe_forward_bf16 (it selects the expert products' arithmetic).
  * shared_stream (nullable, like the reference engine's shared_stream,
  * k3_engine.cu:1668-1689) takes the latent projection and the shared
- * expert's gate/up while `stream` routes; the call joins it back with
- * events before the shared down projection, so the result and its
- * completion on `stream` are the same as without it. The fork/join events
- * are created once per host thread and device (no device memory). */
+ * expert's gate/up while `stream` routes; the call joins it back with events before the shared
+ * down projection, so the result and its completion on `stream` are the
+ * same as without it. The fork/join events are created once per host
+ * thread and device (no device memory). The event calls cost host time
+ * (tens of microseconds per call on ROCm 7): at one token the layer is
+ * then host-bound, so an eager caller is faster without it and a caller
+ * that captures the call in a graph faster with it. */
 bool k3_moe_native_forward_bf16(void *output, const void *hidden, const void *residual,
                                 const k3_moe_native_weights *weights,
                                 const k3_moe_native_shape *shape, uint32_t token_count,

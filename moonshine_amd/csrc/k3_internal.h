@@ -24,6 +24,12 @@ bool q8_gemv_fits(uint32_t cols, const void *codes, const void *x);
 bool launch_q8_gemv(uint16_t *out, const void *codes, const void *scales, const void *x,
                     uint32_t rows, uint32_t cols, const uint16_t *add1, const uint16_t *add2,
                     hipStream_t stream);
+/* launch_q8_gemv on rms_norm(x, norm_weight, eps) (the RMSNorm entry
+ * point's bits), without the normalised vector ever leaving the kernel.
+ * norm_weight 16-byte aligned. */
+bool launch_q8_gemv_norm(uint16_t *out, const void *codes, const void *scales, const void *x,
+                         const void *norm_weight, float eps, uint32_t rows, uint32_t cols,
+                         hipStream_t stream);
 /* act = bf16(act(bf16(gate . x), bf16(up . x))) for two Q8-128 matrices. */
 bool launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gate_scales,
                       const void *up_codes, const void *up_scales, const void *x, uint32_t rows,

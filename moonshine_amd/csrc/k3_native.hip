@@ -1,9 +1,12 @@
 /*
  * K3-native MoE layer (k3_engine.cu:1549-1563 router, 1668-1689 latent
  * projection and shared expert, 1851-1897 routed tail and residual): a
- * host-side composition of the library's entry points on one stream, into
- * a caller-provided workspace. Every step is the entry point of the same
- * operation, so intermediates are bit-identical to calling them in order.
+ * host-side composition of the library's kernels on one stream (or two:
+ * the latent projection and the shared expert's gate/up on a second one),
+ * into a caller-provided workspace. Every step computes the same bits as
+ * the entry point of the same operation; at one token the norm runs inside
+ * the up projection and the adds inside the shared down projection's
+ * epilogue.
  */
 #include "../../include/k3_moe.h"
 #include "../../include/k3_rocm_ops.h"
@@ -197,9 +200,19 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
              k3_moe_experts_bf16(ws.routed, ws.latent, nullptr, ws.ids, ws.weights, W.experts,
                                  &s.routed, T, precision, ws.experts, ws.expert_bytes, st);
     }
-    ok = ok &&
-         k3_rocm_rms_norm_bf16(ws.normed, ws.routed, W.routed_norm, T, D, s.norm_epsilon, st) &&
-         project(W.routed_up, ws.full, ws.normed, T, st);
+    /* one token with Q8-128 up weights: the norm runs inside the up
+     * projection (same bits as the separate norm) */
+    if (T == 1u && W.routed_up.kind == K3_MOE_STATIC_Q8_128 &&
+        k3::q8_gemv_fits(D, W.routed_up.data, ws.routed) &&
+        ((uintptr_t)W.routed_norm % 16u) == 0u) {
+        ok = ok && k3::launch_q8_gemv_norm(ws.full, W.routed_up.data, W.routed_up.scales,
+                                           ws.routed, W.routed_norm, s.norm_epsilon, H, D, st);
+    } else {
+        ok = ok &&
+             k3_rocm_rms_norm_bf16(ws.normed, ws.routed, W.routed_norm, T, D, s.norm_epsilon,
+                                   st) &&
+             project(W.routed_up, ws.full, ws.normed, T, st);
+    }
     if (ev) ok = ok && hipStreamWaitEvent(st, ev->act, 0) == hipSuccess;
     if (fused) {
         ok = ok && k3::launch_q8_gemv((uint16_t *)output, W.shared_down.data,

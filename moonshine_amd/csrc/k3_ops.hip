@@ -420,39 +420,103 @@ bool launch_q8_rows(void *out, const void *q, const void *s, const void *x, uint
     return hipGetLastError() == hipSuccess;
 }
 
-/*
- * Single-vector Q8-128 projections for cols <= 8192 (four 64-group K
- * stripes, one per wave), R rows per block of 256 threads. Each lane loads
- * its group of x once for all R rows; the unscaled group sums and their
- * scales meet in LDS, and lane l then chains acc = fmaf(gs, scale, acc)
- * over its groups l, l + 64, ... in order -- exactly q8_rows_kernel's per
- * lane sequence -- before the same wave64 butterfly, so the outputs are
- * bit-identical to it. One wave per row re-read x from L2 for every row,
- * twice the bytes of the int8 weight row itself.
- *
- * DUAL: rows r of two matrices (gate, up) per block and out = bf16(act(
- * bf16(gate), bf16(up))), the shared expert's gate/up/activation in one
- * pass. Otherwise out = bf16(v), or with the epilogue addends
- * bf16(add2 + bf16(add1 + bf16(v))) (two bf16 adds, in that order).
- */
-constexpr int kQ8Rows = 8;
+/* RMSNorm pieces shared by rms_norm_kernel and the normalising GEMV, so
+ * that both produce the same bits. Thread t of a 256-thread block owns the
+ * 8-element chunks t + 256 j (j < kRmsChunks) of the vector. */
+constexpr int kRmsChunks = 4; /* 8-element chunks per thread: hidden <= 8192 */
 
-template <bool DUAL>
+__device__ __forceinline__ float rms_sumsq(const uint4 (&xv)[kRmsChunks], uint32_t t,
+                                           uint32_t chunks) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRmsChunks; j++) {
+        if (t + 256u * (uint32_t)j < chunks) {
+            const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                s = fmaf(bf16_lo(u[q]), bf16_lo(u[q]), s);
+                s = fmaf(bf16_hi(u[q]), bf16_hi(u[q]), s);
+            }
+        }
+    }
+    return s;
+}
+
+/* 1 / sqrt(total / hidden + eps) from the four per-wave sums. */
+__device__ __forceinline__ float rms_inv(const float (&part)[4], uint32_t hidden, float eps) {
+    const float total = __fadd_rn(__fadd_rn(part[0], part[1]), __fadd_rn(part[2], part[3]));
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)hidden), eps)));
+}
+
+/* Two packed bf16 of x, scaled: bf16((x * inv) * w). */
+__device__ __forceinline__ uint32_t rms_apply2(uint32_t u, uint32_t w, float inv) {
+    const uint32_t lo = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_lo(u), inv), bf16_lo(w)));
+    const uint32_t hi = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_hi(u), inv), bf16_hi(w)));
+    return lo | (hi << 16);
+}
+
+/*
+ * Single-vector Q8-128 projections for cols <= 8192, R rows per row set
+ * and RS row sets per block of 256 threads: the 4 / RS waves of a row set
+ * split K into 64-group stripes (RS = 2 needs cols <= 4096, RS = 4 cols <=
+ * 2048). Each lane loads its group of x once for all R rows; the unscaled
+ * group sums and their scales meet in LDS, and lane l then chains acc =
+ * fmaf(gs, scale, acc) over its groups l, l + 64, ... in order -- exactly
+ * q8_rows_kernel's per lane sequence -- before the same wave64 butterfly,
+ * so the outputs are bit-identical to it. One wave per row re-read x from
+ * L2 for every row, twice the bytes of the int8 weight row itself.
+ *
+ * DUAL (RS = 1): rows r of two matrices (gate, up) per block and out =
+ * bf16(act(bf16(gate), bf16(up))), the shared expert's gate/up/activation
+ * in one pass. Otherwise out = bf16(v), or with the epilogue addends
+ * bf16(add2 + bf16(add1 + bf16(v))) (two bf16 adds, in that order).
+ *
+ * NORM: x is first replaced by rms_norm_kernel's output for (x, norm_w,
+ * eps), bit for bit: every block recomputes the sum of squares in that
+ * kernel's order from the vector and norm weight it loads before the
+ * weight rows, normalises its own chunks into LDS and reads its groups
+ * back, which saves the norm's launch and its round trip through memory.
+ */
+constexpr int kQ8DualRows = 8; /* rows per block of the DUAL kernel */
+
+template <bool DUAL, int R, int RS, bool NORM>
 __global__ __launch_bounds__(256) void q8_gemv_kernel(
         uint16_t *__restrict__ out, const int8_t *__restrict__ codes_a,
         const float *__restrict__ scales_a, const int8_t *__restrict__ codes_b,
         const float *__restrict__ scales_b, const uint16_t *__restrict__ x, uint32_t rows,
         uint32_t cols, uint32_t align16, const uint16_t *__restrict__ add1,
-        const uint16_t *__restrict__ add2, uint32_t act_kind, float beta, float lb) {
-    constexpr int R = kQ8Rows, NM = DUAL ? 2 : 1;
-    __shared__ float part[NM * R][4][64];
-    __shared__ float scl[NM * R][4][64];
+        const uint16_t *__restrict__ add2, uint32_t act_kind, float beta, float lb,
+        const uint16_t *__restrict__ norm_w, float eps) {
+    static_assert(RS == 1 || RS == 2 || RS == 4, "row sets");
+    static_assert(!DUAL || RS == 1, "DUAL uses one row set");
+    constexpr int NM = DUAL ? 2 : 1, SPS = 4 / RS, RB = R * RS;
+    static_assert(RB >= 4, "at least one row per wave in the reduction");
+    __shared__ float part[NM * RB][SPS][64];
+    __shared__ float scl[NM * RB][SPS][64];
+    __shared__ float npart[4];
+    __shared__ uint4 xn[NORM ? 8192 / 8 : 1]; /* the normalised vector */
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t row0 = blockIdx.x * R;
-    const uint32_t groups = cols / 32u, g = 64u * wave + lane;
-    if (g < groups) {
-        uint4 wa[NM * R], wb[NM * R];
-        float sc[NM * R];
+    const uint32_t set = wave / SPS, stripe = wave % SPS;
+    const uint32_t row0 = blockIdx.x * RB + set * R;
+    const uint32_t groups = cols / 32u, g = 64u * stripe + lane;
+    const bool active = g < groups;
+    /* NORM: the vector and the norm weight first, so that waiting for them
+     * does not wait for the weight rows (loads complete in issue order) */
+    uint4 xv[NORM ? kRmsChunks : 1], nv[NORM ? kRmsChunks : 1];
+    const uint32_t chunks = cols / 8u;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int j = 0; j < kRmsChunks; j++) {
+            const uint32_t c = threadIdx.x + 256u * (uint32_t)j;
+            if (c < chunks) {
+                xv[j] = ((const uint4 *)x)[c];
+                nv[j] = ((const uint4 *)norm_w)[c];
+            }
+        }
+    }
+    uint4 wa[NM * R], wb[NM * R];
+    float sc[NM * R];
+    if (active) {
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const int8_t *q = m ? codes_b : codes_a;
@@ -465,38 +529,65 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(
                 sc[m * R + i] = sp[(uint64_t)r * (cols / 128u) + (g >> 2)];
             }
         }
-        float xf[32];
-        bf16x32_to_f32((const uint4 *)x + 4u * g, xf);
+    }
+    float xf[32];
+    if constexpr (NORM) {
+        /* rms_norm_kernel's sum, then each thread normalises its own chunks
+         * into LDS and every lane reads its group back */
+        const uint32_t t = threadIdx.x;
+        const float s = wave_sum(rms_sumsq(xv, t, chunks));
+        if (lane == 0u) npart[wave] = s;
+        __syncthreads();
+        const float inv = rms_inv(npart, cols, eps);
 #pragma unroll
-        for (int i = 0; i < NM * R; i++) {
-            part[i][wave][lane] = q8_group(wa[i], wb[i], xf);
-            scl[i][wave][lane] = sc[i];
+        for (int j = 0; j < kRmsChunks; j++) {
+            const uint32_t c = t + 256u * (uint32_t)j;
+            if (c < chunks)
+                xn[c] = make_uint4(rms_apply2(xv[j].x, nv[j].x, inv),
+                                   rms_apply2(xv[j].y, nv[j].y, inv),
+                                   rms_apply2(xv[j].z, nv[j].z, inv),
+                                   rms_apply2(xv[j].w, nv[j].w, inv));
         }
+        __syncthreads();
+        if (active) bf16x32_to_f32(xn + 4u * g, xf);
+    } else {
+        if (active) bf16x32_to_f32((const uint4 *)x + 4u * g, xf);
+    }
+    if (active) {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int pr = m * RB + (int)set * R + i;
+                part[pr][stripe][lane] = q8_group(wa[m * R + i], wb[m * R + i], xf);
+                scl[pr][stripe][lane] = sc[m * R + i];
+            }
     }
     __syncthreads();
-    constexpr int RPW = R / 4; /* rows per wave in the reduction */
+    constexpr int RPW = RB / 4; /* rows per wave (per matrix) in the reduction */
     const uint32_t stripes = (groups + 63u) / 64u;
     float p[NM * RPW];
 #pragma unroll
     for (int q = 0; q < NM * RPW; q++) {
-        const int i = (q / RPW) * R + (int)wave * RPW + (q % RPW);
+        const int i = (q / RPW) * RB + (int)wave * RPW + (q % RPW);
         float acc = 0.0f;
         for (uint32_t j = 0; j < stripes; j++)
             if (64u * j + lane < groups) acc = fmaf(part[i][j][lane], scl[i][j][lane], acc);
         p[q] = acc;
     }
     const float v = wave_sum_rows<NM * RPW>(p);
+    const uint32_t base = blockIdx.x * RB + RPW * wave;
     if constexpr (DUAL) {
         /* lanes < 32: gate rows, lanes >= 32: the same up rows */
         const float u = __shfl_xor(v, 32, 64);
         const float gb = bf16_to_f32(f32_to_bf16(v)), ub = bf16_to_f32(f32_to_bf16(u));
         constexpr uint32_t kSpan = 32u / RPW;
-        const uint32_t row = row0 + RPW * wave + lane / kSpan;
+        const uint32_t row = base + lane / kSpan;
         if (lane < 32u && (lane & (kSpan - 1u)) == 0u && row < rows)
             out[row] = f32_to_bf16(gated_act(gb, ub, act_kind, beta, lb));
     } else {
         const int owner = wave_rows_owner<RPW>();
-        const uint32_t row = row0 + RPW * wave + (uint32_t)owner;
+        const uint32_t row = base + (uint32_t)owner;
         if ((lane & (64u / RPW - 1u)) == 0u && row < rows) {
             float r = bf16_to_f32(f32_to_bf16(v));
             if (add1) r = bf16_to_f32(f32_to_bf16(__fadd_rn(bf16_to_f32(add1[row]), r)));
@@ -595,8 +686,6 @@ __global__ void add_kernel(uint16_t *__restrict__ out, const uint16_t *__restric
  * weight). hidden <= 8192 with 16-byte rows keeps the vector in registers
  * (every load issued up front: one memory round trip); otherwise the same
  * order element by element. */
-constexpr int kRmsChunks = 4; /* 8-element chunks per thread: hidden <= 8192 */
-
 __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t *__restrict__ out,
                                                        const uint16_t *__restrict__ in,
                                                        const uint16_t *__restrict__ weight,
@@ -606,7 +695,6 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t *__restrict__ ou
     const uint16_t *x = in + (uint64_t)blockIdx.x * hidden;
     uint16_t *o = out + (uint64_t)blockIdx.x * hidden;
     const uint32_t chunks = (hidden + 7u) / 8u;
-    float s = 0.0f;
     if (vec) {
         uint4 xv[kRmsChunks], wv[kRmsChunks];
 #pragma unroll
@@ -617,40 +705,22 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t *__restrict__ ou
                 wv[j] = ((const uint4 *)weight)[c];
             }
         }
-#pragma unroll
-        for (int j = 0; j < kRmsChunks; j++) {
-            if (t + 256u * (uint32_t)j < chunks) {
-                const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    s = fmaf(bf16_lo(u[q]), bf16_lo(u[q]), s);
-                    s = fmaf(bf16_hi(u[q]), bf16_hi(u[q]), s);
-                }
-            }
-        }
-        s = wave_sum(s);
+        const float s = wave_sum(rms_sumsq(xv, t, chunks));
         if ((t & 63u) == 0u) part[t >> 6] = s;
         __syncthreads();
-        const float total = __fadd_rn(__fadd_rn(part[0], part[1]), __fadd_rn(part[2], part[3]));
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)hidden), eps)));
+        const float inv = rms_inv(part, hidden, eps);
 #pragma unroll
         for (int j = 0; j < kRmsChunks; j++) {
             const uint32_t c = t + 256u * (uint32_t)j;
-            if (c < chunks) {
-                const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-                const uint32_t w[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-                uint32_t r[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t lo = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_lo(u[q]), inv), bf16_lo(w[q])));
-                    const uint32_t hi = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_hi(u[q]), inv), bf16_hi(w[q])));
-                    r[q] = lo | (hi << 16);
-                }
-                ((uint4 *)o)[c] = make_uint4(r[0], r[1], r[2], r[3]);
-            }
+            if (c < chunks)
+                ((uint4 *)o)[c] = make_uint4(rms_apply2(xv[j].x, wv[j].x, inv),
+                                             rms_apply2(xv[j].y, wv[j].y, inv),
+                                             rms_apply2(xv[j].z, wv[j].z, inv),
+                                             rms_apply2(xv[j].w, wv[j].w, inv));
         }
         return;
     }
+    float s = 0.0f;
     for (uint32_t c = t; c < chunks; c += 256u) {
         const uint32_t end = 8u * c + 8u < hidden ? 8u * c + 8u : hidden;
         for (uint32_t d = 8u * c; d < end; d++) {
@@ -661,8 +731,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t *__restrict__ ou
     s = wave_sum(s);
     if ((t & 63u) == 0u) part[t >> 6] = s;
     __syncthreads();
-    const float total = __fadd_rn(__fadd_rn(part[0], part[1]), __fadd_rn(part[2], part[3]));
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)hidden), eps)));
+    const float inv = rms_inv(part, hidden, eps);
     for (uint32_t d = t; d < hidden; d += 256u)
         o[d] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(x[d]), inv), bf16_to_f32(weight[d])));
 }
@@ -1000,15 +1069,55 @@ bool k3::q8_gemv_fits(uint32_t cols, const void *codes, const void *x) {
            ((uintptr_t)x % 16u) == 0u;
 }
 
+namespace {
+
+template <int R, int RS, bool NORM>
+void q8_gemv_launch(uint16_t *out, const void *codes, const void *scales, const void *x,
+                    uint32_t rows, uint32_t cols, uint32_t align16, const uint16_t *add1,
+                    const uint16_t *add2, const uint16_t *norm_w, float eps, hipStream_t st) {
+    constexpr uint32_t rb = R * RS;
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<false, R, RS, NORM>), dim3((rows + rb - 1u) / rb),
+                       dim3(256), 0, st, out, (const int8_t *)codes, (const float *)scales,
+                       nullptr, nullptr, (const uint16_t *)x, rows, cols, align16, add1, add2, 0u,
+                       1.0f, 1.0f, norm_w, eps);
+}
+
+/* Row blocking measured on cold weights (one MI355X): 4 rows per set beats
+ * 8 and 16 on every single-matrix shape of the K3 layer (e.g. 7168 x 6144:
+ * 10.6 us against 13.3 us for 8 rows), as more, smaller blocks spread the
+ * stream over all CUs; with the norm prologue two row sets per block pay
+ * it over 8 rows (7168 x 3584: 9.6 us against 12.3 us for one set). */
+template <bool NORM>
+void q8_gemv_dispatch(uint16_t *out, const void *codes, const void *scales, const void *x,
+                      uint32_t rows, uint32_t cols, uint32_t align16, const uint16_t *add1,
+                      const uint16_t *add2, const uint16_t *norm_w, float eps, hipStream_t st) {
+    if (NORM && cols <= 4096u)
+        q8_gemv_launch<4, 2, NORM>(out, codes, scales, x, rows, cols, align16, add1, add2, norm_w, eps, st);
+    else
+        q8_gemv_launch<4, 1, NORM>(out, codes, scales, x, rows, cols, align16, add1, add2, norm_w, eps, st);
+}
+
+}  // namespace
+
 bool k3::launch_q8_gemv(uint16_t *out, const void *codes, const void *scales, const void *x,
                         uint32_t rows, uint32_t cols, const uint16_t *add1, const uint16_t *add2,
                         hipStream_t st) {
     if (!q8_gemv_fits(cols, codes, x) || rows == 0u) return false;
     const uint32_t align16 = ((uintptr_t)codes % 16u) == 0u;
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<false>), dim3((rows + kQ8Rows - 1u) / kQ8Rows),
-                       dim3(256), 0, st, out, (const int8_t *)codes, (const float *)scales,
-                       nullptr, nullptr, (const uint16_t *)x, rows, cols, align16, add1, add2, 0u,
-                       1.0f, 1.0f);
+    q8_gemv_dispatch<false>(out, codes, scales, x, rows, cols, align16, add1, add2, nullptr, 0.0f,
+                            st);
+    return hipGetLastError() == hipSuccess;
+}
+
+bool k3::launch_q8_gemv_norm(uint16_t *out, const void *codes, const void *scales, const void *x,
+                             const void *norm_weight, float eps, uint32_t rows, uint32_t cols,
+                             hipStream_t st) {
+    if (!q8_gemv_fits(cols, codes, x) || rows == 0u || !norm_weight ||
+        ((uintptr_t)norm_weight % 16u) != 0u)
+        return false;
+    const uint32_t align16 = ((uintptr_t)codes % 16u) == 0u;
+    q8_gemv_dispatch<true>(out, codes, scales, x, rows, cols, align16, nullptr, nullptr,
+                           (const uint16_t *)norm_weight, eps, st);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -1019,9 +1128,10 @@ bool k3::launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gat
     if (!q8_gemv_fits(cols, gate_codes, x) || !q8_gemv_fits(cols, up_codes, x) || rows == 0u)
         return false;
     const uint32_t align16 = (((uintptr_t)gate_codes | (uintptr_t)up_codes) % 16u) == 0u;
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<true>), dim3((rows + kQ8Rows - 1u) / kQ8Rows),
-                       dim3(256), 0, st, act, (const int8_t *)gate_codes, (const float *)gate_scales,
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<true, kQ8DualRows, 1, false>),
+                       dim3((rows + kQ8DualRows - 1u) / kQ8DualRows), dim3(256), 0, st, act,
+                       (const int8_t *)gate_codes, (const float *)gate_scales,
                        (const int8_t *)up_codes, (const float *)up_scales, (const uint16_t *)x, rows,
-                       cols, align16, nullptr, nullptr, kind, beta, lb);
+                       cols, align16, nullptr, nullptr, kind, beta, lb, nullptr, 0.0f);
     return hipGetLastError() == hipSuccess;
 }

@@ -132,6 +132,41 @@ def test_decode_layer_bitexact(cuda, cfg):
 
 
 
+def test_decode_graph_replay_same_bits(cuda):
+    """Decode calls captured in a HIP graph give the oracle's bits on every
+    replay, with eager calls on the same workspace between the replays."""
+    import dataclasses
+    cfg = CONFIGS[1]
+    a = make_inputs(cfg)
+    other = make_inputs(cfg, seed=cfg.seed + 5)
+    b = dataclasses.replace(a, hidden=other.hidden, residual=other.residual)
+    moe = get_layer(cfg, a, cuda)
+    wants = []
+    for inp in (a, b):
+        ids = O.router_topk(O.router_logits(inp.router_weight, inp.hidden), inp.router_bias,
+                            cfg.top_k, cfg.scale)[0]
+        wants.append(O.layer(cfg, inp, host_experts(moe.store, ids))["output"])
+    xa, ra = L.bf16_tensor(a.hidden, cuda), L.bf16_tensor(a.residual, cuda)
+    out = torch.zeros_like(xa)
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        moe.forward(xa, ra, out=out, stream=cap.cuda_stream)
+        cap.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            moe.forward(xa, ra, out=out, stream=cap.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(L.bf16_bits(out), wants[0], err_msg=f"replay {rep}")
+        o2, _, _ = run(cfg, b, moe, cuda)  # eager, same layer and workspace
+        np.testing.assert_array_equal(o2, wants[1])
+
+
 @pytest.mark.parametrize("T", [1, 5])
 def test_missing_routes(cuda, T):
     """Only two experts selectable (NaN bias elsewhere) with top_k = 4: the

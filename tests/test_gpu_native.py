@@ -96,3 +96,49 @@ def test_native_shared_stream_same_bits(cuda, T):
         out = layer.forward(dx[i], dr[i], shared_stream=side.cuda_stream)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(bf16_bits(out), want[i])
+
+
+@pytest.mark.parametrize("streams", [1, 2])
+def test_native_graph_replay_same_bits(cuda, streams):
+    """One-token calls captured in a HIP graph (with and without the shared
+    stream) give the oracle's bits on every replay, with eager calls that
+    reuse the workspace between the replays."""
+    layer = N.NativeLayer(SMALL, device=cuda)
+    side = torch.cuda.Stream()
+    rng = np.random.default_rng(91 + streams)
+    xs = [f32_to_bf16_bits(rng.normal(0, 1, (1, SMALL.hidden)).astype(np.float32)) for _ in range(3)]
+    rs = [f32_to_bf16_bits(rng.normal(0, 1, (1, SMALL.hidden)).astype(np.float32)) for _ in range(3)]
+    statics = host_statics(layer)
+    want = []
+    for x, r in zip(xs, rs):
+        ids = O.router_topk(O.router_logits(layer.router_weight_bits, x), layer.router_bias,
+                            SMALL.top_k, SMALL.scale)[0]
+        experts = {int(e): layer.store.host_expert(int(e)) for e in np.unique(ids)}
+        want.append(O.native_layer(SMALL, layer.router_weight_bits, layer.router_bias,
+                                   layer.norm_bits, statics, x, r, experts)["output"])
+    dx = [bf16_tensor(x, cuda) for x in xs]
+    dr = [bf16_tensor(r, cuda) for r in rs]
+    outs = [torch.zeros_like(dx[0]) for _ in range(2)]
+    shared = side.cuda_stream if streams == 2 else None
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        layer.forward(dx[0], dr[0], out=outs[0], stream=cap.cuda_stream, shared_stream=shared)
+        cap.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(2):
+                layer.forward(dx[i], dr[i], out=outs[i], stream=cap.cuda_stream,
+                              shared_stream=shared)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            np.testing.assert_array_equal(bf16_bits(outs[i]), want[i], err_msg=f"replay {rep}")
+        eager = layer.forward(dx[2], dr[2])  # eager work on the same workspace
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bf16_bits(eager), want[2])

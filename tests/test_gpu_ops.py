@@ -349,7 +349,8 @@ def test_q8_quantize_dequantize_bitexact(cuda):
     assert not ops.k3_rocm_bf16_quantize_q8_128(q, s, dev(wb.view(np.int16), cuda), rows, 1000)
 
 
-@pytest.mark.parametrize("T,rows,cols", [(1, 3584, 7168), (1, 7168, 3584), (3, 96, 1024),
+@pytest.mark.parametrize("T,rows,cols", [(1, 3584, 7168), (1, 7168, 3584), (1, 77, 4096),
+                                         (1, 100, 2048), (1, 50, 256), (3, 96, 1024),
                                          (17, 64, 6144), (64, 33, 2048)])
 def test_q8_gemm_bitexact(cuda, T, rows, cols):
     rng = np.random.default_rng(rows * 7 + cols + T)
