@@ -115,6 +115,25 @@ bool k3_moe_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
                        size_t scratch_bytes, void *stream);
 
 /*
+ * Routes of a token batch, replacing the prefill router pair
+ * k3_rocm_bf16_gemm_f32 + k3_rocm_router_topk_f32_batch
+ * (k3_engine_prefill.inc:1448-1460) with the same ids and weights, bit for
+ * bit. From 128 tokens on (hidden % 64 == 0, hidden <= 8192, expert_count
+ * <= 1024, 16-byte aligned hidden and router_weight) the logits run on bf16
+ * MFMA and each token recomputes in the exact order only the experts that a
+ * rigorous error bound cannot rule out of its top-k; otherwise the exact
+ * logits and top-k kernels run. expert_ids / expert_weights: [T, k] (may be
+ * host-mapped). scratch: k3_moe_router_scratch_bytes(T, E) bytes of device
+ * memory (256-byte aligned). token_count <= 65535.
+ */
+size_t k3_moe_router_scratch_bytes(uint32_t token_count, uint32_t expert_count);
+bool k3_moe_router_bf16(uint32_t *expert_ids, float *expert_weights, const void *hidden,
+                        const void *router_weight, const void *router_bias,
+                        uint32_t token_count, uint32_t expert_count, uint32_t hidden_size,
+                        uint32_t top_k, float scaling_factor, void *scratch,
+                        size_t scratch_bytes, void *stream);
+
+/*
  * The whole routed-MoE layer for token_count rows:
  *   logits = router_weight[E, H] . hidden[t]        (f32)
  *   ids, weights = top-k(sigmoid(logits) + bias)    (k3_rocm_router_topk)

@@ -110,6 +110,8 @@ SIGNATURES = {
                                         _p, _sz, _p, _p]),
     "k3_moe_workspace_init": (_b, [_p, _sz, _p]),
     "k3_moe_plan_scratch_bytes": (_sz, [_u32, _u32]),
+    "k3_moe_router_scratch_bytes": (_sz, [_u32, _u32]),
+    "k3_moe_router_bf16": (_b, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _f, _p, _sz, _p]),
     "k3_moe_route_plan": (_b, [_p, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _p, _sz, _p]),
     "k3_moe_forward_bf16": (_b, [_p, _p, _p, _p, _p, _p, ctypes.POINTER(K3MoeShape), _u32,
                                  _u32, _p, _p, _p, _sz, _p]),

@@ -35,6 +35,19 @@ bool launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gate_sc
                       const void *up_codes, const void *up_scales, const void *x, uint32_t rows,
                       uint32_t cols, uint32_t kind, float beta, float lb, hipStream_t stream);
 
+/* Certified MFMA router for token batches (k3_router.hip): the exact
+ * router's routes and weights, with the logit GEMM on bf16 MFMA. approx
+ * holds T x E floats, norms E floats. mark (nullable) is called with the
+ * top-k stage between the logits and the selection. */
+struct StageMarker;
+bool router_certified_supported(uint32_t tokens, uint32_t experts, uint32_t hidden,
+                                uint32_t top_k, const void *router_weight, const void *x);
+bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, float *w2,
+                             float *approx, float *norms, const void *router_weight,
+                             const void *router_bias, const void *x, uint32_t T, uint32_t E,
+                             uint32_t H, uint32_t k, float scale, hipStream_t stream,
+                             const StageMarker *mark);
+
 /* Router top-k; ids2/w2 (nullable) receive extra copies (e.g. mapped host
  * memory) while ids/w stay in device memory for later kernels. */
 bool launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,

@@ -630,6 +630,27 @@ extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void
                        StageMarker{nullptr, st});
 }
 
+/* Routes of a token batch into ws.ids / ws.weights (and the caller's
+ * copies): the certified MFMA router from kCertifiedMinTokens tokens on,
+ * the exact w64 logits + top-k below that; both give the same bits. */
+static constexpr uint32_t kCertifiedMinTokens = 128;
+
+static bool route_batch(const Workspace &ws, const void *hidden, const void *router_weight,
+                 const void *router_bias, const k3_moe_shape &s, uint32_t T, void *expert_ids,
+                 void *expert_weights, hipStream_t st, const StageMarker *mark) {
+    const uint32_t E = s.expert_count, H = s.hidden, k = s.top_k;
+    if (T >= kCertifiedMinTokens && router_certified_supported(T, E, H, k, router_weight, hidden))
+        return launch_router_certified(ws.ids, ws.weights, (uint32_t *)expert_ids,
+                                       (float *)expert_weights, ws.logits, ws.scores,
+                                       router_weight, router_bias, hidden, T, E, H, k,
+                                       s.scaling_factor, st, mark);
+    if (!launch_bf16_rows_f32_any(ws.logits, router_weight, hidden, T, E, H, st)) return false;
+    if (mark) (*mark)(K3_MOE_STAGE_TOPK);
+    return launch_router_topk(ws.ids, ws.weights, (uint32_t *)expert_ids, (float *)expert_weights,
+                              ws.logits, (const float *)router_bias, T, E, k, s.scaling_factor,
+                              st);
+}
+
 extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, const void *residual,
                                     const void *router_weight, const void *router_bias,
                                     const k3_moe_expert *experts, const k3_moe_shape *shape,
@@ -651,12 +672,8 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
         return decode_launch(P, st, mark);
     }
     mark(K3_MOE_STAGE_ROUTER);
-    if (!launch_bf16_rows_f32_any(ws.logits, router_weight, hidden, token_count,
-                                  shape->expert_count, shape->hidden, st) ||
-        (mark(K3_MOE_STAGE_TOPK), false) ||
-        !launch_router_topk(ws.ids, ws.weights, (uint32_t *)expert_ids, (float *)expert_weights,
-                            ws.logits, (const float *)router_bias, token_count,
-                            shape->expert_count, shape->top_k, shape->scaling_factor, st))
+    if (!route_batch(ws, hidden, router_weight, router_bias, *shape, token_count, expert_ids,
+                     expert_weights, st, &mark))
         return false;
     return run_experts(ws, output, hidden, residual, experts, *shape, token_count, precision, st,
                        mark);

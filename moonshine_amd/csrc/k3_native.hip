@@ -23,7 +23,7 @@ constexpr size_t kAlign = 256;
 size_t up256(size_t n) { return (n + kAlign - 1u) & ~(kAlign - 1u); }
 
 struct NativeWorkspace {
-    float *logits;
+    float *logits, *norms;
     uint32_t *ids;
     float *weights;
     uint16_t *latent, *routed, *normed, *full, *gate, *up, *act, *shared, *sum;
@@ -43,6 +43,7 @@ NativeWorkspace carve(void *base, const k3_moe_native_shape &s, uint32_t T) {
     const size_t D = s.routed.hidden, H = s.model_hidden, S = s.shared_hidden;
     const size_t E = s.routed.expert_count, k = s.routed.top_k;
     w.logits = (float *)take(4u * T * E);
+    w.norms = (float *)take(4u * E);
     w.ids = (uint32_t *)take(4u * T * k);
     w.weights = (float *)take(4u * T * k);
     w.latent = (uint16_t *)take(2u * T * D);
@@ -193,9 +194,18 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
                                              ev ? ev->latent : nullptr, st);
         routes_copied = true;
     } else {
-        ok = ok && k3_rocm_bf16_gemm_f32(ws.logits, W.router_weight, hidden, T, E, H, st) &&
-             k3_rocm_router_topk_f32_batch(ws.ids, ws.weights, ws.logits, W.router_bias, T, E,
-                                           k, s.routed.scaling_factor, st) &&
+        /* token batches: the certified MFMA router (same routes) */
+        const bool cert = T >= 128u && k3::router_certified_supported(T, E, H, k,
+                                                                       W.router_weight, hidden);
+        ok = ok &&
+             (cert ? k3::launch_router_certified(ws.ids, ws.weights, nullptr, nullptr, ws.logits,
+                                                 ws.norms, W.router_weight, W.router_bias,
+                                                 hidden, T, E, H, k, s.routed.scaling_factor,
+                                                 st, nullptr)
+                   : k3_rocm_bf16_gemm_f32(ws.logits, W.router_weight, hidden, T, E, H, st) &&
+                         k3_rocm_router_topk_f32_batch(ws.ids, ws.weights, ws.logits,
+                                                       W.router_bias, T, E, k,
+                                                       s.routed.scaling_factor, st)) &&
              (!ev || hipStreamWaitEvent(st, ev->latent, 0) == hipSuccess) &&
              k3_moe_experts_bf16(ws.routed, ws.latent, nullptr, ws.ids, ws.weights, W.experts,
                                  &s.routed, T, precision, ws.experts, ws.expert_bytes, st);

@@ -1,0 +1,511 @@
+/*
+ * Certified MFMA router for token batches (prefill). The routes and weights
+ * are those of the exact router -- logits in the w64 order
+ * (bf16_rows_f32_kernel / bf16_gemm_w64_kernel, k3_rocm_ops.cu:359-425,
+ * 512-661) followed by router_topk_kernel (k3_rocm_ops.cu:1361-1450) -- bit
+ * for bit, while the logit GEMM runs on bf16 MFMA:
+ *
+ *   router_norms_kernel    n_e >= ||w_e|| for every router row
+ *   router_mfma_kernel     approximate logits a_te = x_t . w_e (bf16 MFMA,
+ *                          fp32 accumulate, any summation order)
+ *   router_certify_kernel  one wave per token: candidates from the
+ *                          approximate logits and a rigorous error bound,
+ *                          exact w64-order logits for the candidates only,
+ *                          then the exact router's top-k on exact keys
+ *
+ * Why the routes are exact. Let p_i = w_i x_i (exact in fp32: bf16 x bf16
+ * products have 16 significant bits), u = 2^-24. Each MFMA instruction sums
+ * a fresh block of 32 products (its C operand is zero); whatever order and
+ * rounding the unit uses inside, its result is taken to be within 4 u per
+ * term, 128 u sum|p_block|, of the block's real sum (a truncating or
+ * block-aligned adder of fp32 width stays within 2 u per term). The H / 32
+ * block results are added in fp32 on the VALU (H / 32 roundings), and the
+ * exact w64 chain has <= 128 fmaf roundings per lane plus a 6-level
+ * butterfly. The kernel uses err_e = (H / 32 + 270) u (1 + 2^-10) n_e
+ * ||x_t||, which covers both sums' errors together, since sum|p_i| <=
+ * ||w_e|| ||x_t|| (Cauchy-Schwarz). The choice is sigmoid(l) +
+ * bias: the real sigmoid's slope on [a - err, a + err] is at most
+ * s'(max(0, |a| - err)) (the slope falls away from 0), the deterministic
+ * sigmoid is within a few ulp of the real one and the bias add rounds once,
+ * so the approximate and exact choices differ by at most ce_e = s'(..)
+ * err_e + 2e-6 + 2^-21 |c_e|. If T_k is the k-th largest approximate choice
+ * and E_k the largest ce among the experts at or above it, those k experts
+ * have exact choices >= T_k - E_k, so every expert of the exact top-k (ties
+ * included) has approximate choice + ce_e >= T_k - E_k. Those are the candidates; every other expert gets key 0
+ * (never selected) and the candidates get their exact keys, so
+ * topk_select_wave returns what it returns on all exact keys. A token with
+ * any non-finite input, approximate logit, norm or bias takes every expert
+ * as a candidate (the exact router on that token).
+ */
+#include "k3_decode.h"
+#include "k3_device.h"
+#include "k3_internal.h"
+#include "k3_topk.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k3 {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+/* inflation that makes a computed fp32 norm an upper bound of the real one
+ * (chains of <= 134 roundings: relative error < 2^-16) */
+constexpr float kNormInflate = 1.0f + 1.0f / 4096.0f;
+
+/* ---------------------------------------------------------------------- */
+/* row norms                                                               */
+/* ---------------------------------------------------------------------- */
+
+/* One wave per router row: n_e = sqrt(sum w^2) * kNormInflate. */
+__global__ __launch_bounds__(256) void router_norms_kernel(float *__restrict__ norms,
+                                                           const uint16_t *__restrict__ w,
+                                                           uint32_t E, uint32_t H) {
+    const uint32_t lane = threadIdx.x & 63u, e = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (e >= E) return;
+    const uint4 *row = (const uint4 *)(w + (uint64_t)e * H);
+    float s = 0.0f;
+    for (uint32_t c = lane; c < H / 8u; c += 64u) {
+        const uint4 v = row[c];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            s = fmaf(bf16_lo(u[q]), bf16_lo(u[q]), s);
+            s = fmaf(bf16_hi(u[q]), bf16_hi(u[q]), s);
+        }
+    }
+    s = wave_sum(s);
+    if (lane == 0u) norms[e] = __fmul_rn(__fsqrt_rn(s), kNormInflate);
+}
+
+/* ---------------------------------------------------------------------- */
+/* approximate logits on MFMA                                              */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * out[t, e] ~= x_t . w_e, summed as described above (C = 0 MFMAs, fp32
+ * adds of the 32-product blocks). Block tile 128 tokens x 128 experts, 8
+ * waves of 32 x 64 (2 x 4 V_MFMA_F32_16X16X32_BF16 tiles), K steps of 64
+ * staged in two LDS buffers (rows padded to 144 bytes so the 16 rows of a fragment
+ * read fall on different banks). Lane l = 16 g + c supplies row c of a
+ * fragment with the 8 bf16 at K offset 8 g (A: tokens, B: experts; the
+ * same K assignment on both operands, which is all a dot product needs);
+ * it receives tokens 4 g .. 4 g + 3 of expert column c. Rows past T or E
+ * load the last valid row and are not stored. Tiles are dealt to the XCDs
+ * in contiguous ranges, a token tile's expert tiles together, so one XCD's
+ * L2 serves a token tile to all of its expert tiles.
+ */
+constexpr uint32_t kRT = 128, kRK = 64, kRPad = 144;
+
+typedef uint8_t RouterStage[2][kRT * kRPad]; /* [A tokens | B experts] rows */
+
+__device__ __forceinline__ void rt_load(uint4 &a0, uint4 &a1, uint4 &b0, uint4 &b1,
+                                        const uint8_t *xb, const uint8_t *wb,
+                                        const uint32_t (&ao)[2], const uint32_t (&bo)[2],
+                                        uint32_t kb) {
+    /* byte offsets of the thread's two rows (< 2^31: T H 2 bytes) */
+    a0 = *(const uint4 *)(xb + ao[0] + kb);
+    a1 = *(const uint4 *)(xb + ao[1] + kb);
+    b0 = *(const uint4 *)(wb + bo[0] + kb);
+    b1 = *(const uint4 *)(wb + bo[1] + kb);
+}
+
+__device__ __forceinline__ void rt_store(RouterStage &buf, uint32_t off, const uint4 &a0,
+                                         const uint4 &a1, const uint4 &b0, const uint4 &b1) {
+    constexpr uint32_t R64 = 64u * kRPad;
+    *(uint4 *)(buf[0] + off) = a0;
+    *(uint4 *)(buf[0] + off + R64) = a1;
+    *(uint4 *)(buf[1] + off) = b0;
+    *(uint4 *)(buf[1] + off + R64) = b1;
+}
+
+__device__ __forceinline__ void rt_compute(f32x4_t (&acc)[2][4], const RouterStage &buf,
+                                           uint32_t a_off, uint32_t b_off) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        bf16x8_t af[2], bf[4];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            af[i] = __builtin_bit_cast(bf16x8_t, *(const uint4 *)(buf[0] + a_off + 16u * kRPad * i +
+                                                                  64u * ks));
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            bf[j] = __builtin_bit_cast(bf16x8_t, *(const uint4 *)(buf[1] + b_off + 16u * kRPad * j +
+                                                                  64u * ks));
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                /* a fresh 32-term dot product per instruction (C = 0),
+                 * accumulated with one fp32 add per K block */
+                const f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    af[i], bf[j], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[i][j][r] = __fadd_rn(acc[i][j][r], d[r]);
+            }
+    }
+}
+
+/* 8 waves: wave w covers tokens 32 (w / 2) .. + 32 and experts 64 (w % 2)
+ * .. + 64 of the block's 128 x 128 tile. */
+__global__ __launch_bounds__(512) void router_mfma_kernel(float *__restrict__ out,
+                                                          const uint16_t *__restrict__ x,
+                                                          const uint16_t *__restrict__ w,
+                                                          uint32_t T, uint32_t E, uint32_t H) {
+    __shared__ __attribute__((aligned(16))) RouterStage lds[2];
+    const uint32_t ntt = (T + kRT - 1u) / kRT, net = (E + kRT - 1u) / kRT;
+    const uint32_t works = ntt * net, per = (works + 7u) / 8u;
+    const uint32_t L = blockIdx.x, j8 = L >> 3, wk = (L & 7u) * per + j8;
+    if (j8 >= per || wk >= works) return;
+    const uint32_t t0 = (wk / net) * kRT, e0 = (wk % net) * kRT;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1u, g = lane >> 4, c = lane & 15u;
+    /* thread tid loads 16-byte piece tid % 8 of rows tid / 8 and tid / 8 +
+     * 64; rows past T or E clamp to the last one (their results are not
+     * stored) */
+    const uint32_t r0 = tid >> 3, pc = tid & 7u;
+    uint32_t ao[2], bo[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t ta = t0 + r0 + 64u * i, eb = e0 + r0 + 64u * i;
+        ao[i] = ((ta < T ? ta : T - 1u) * H + 8u * pc) * 2u;
+        bo[i] = ((eb < E ? eb : E - 1u) * H + 8u * pc) * 2u;
+    }
+    const uint8_t *xb = (const uint8_t *)x, *wb = (const uint8_t *)w;
+    const uint32_t soff = r0 * kRPad + 16u * pc;
+    const uint32_t a_off = (32u * wm + c) * kRPad + 16u * g;
+    const uint32_t b_off = (64u * wn + c) * kRPad + 16u * g;
+    f32x4_t acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t nsteps = H / kRK, last = nsteps - 1u;
+    /* two register sets: step s + 2's loads are issued at the start of
+     * step s, so each load has two steps of MFMAs to land. Loads and
+     * stores are unconditional (steps past the end reload the last one
+     * into a buffer nobody reads). */
+    uint4 a0, a1, b0, b1, p0, p1, q0, q1;
+    rt_load(a0, a1, b0, b1, xb, wb, ao, bo, 0u);
+    rt_load(p0, p1, q0, q1, xb, wb, ao, bo, 2u * kRK * (1u < last ? 1u : last));
+    rt_store(lds[0], soff, a0, a1, b0, b1);
+    __syncthreads();
+    for (uint32_t s = 0; s < nsteps; s += 2u) {
+        const uint32_t k2 = 2u * kRK * (s + 2u < last ? s + 2u : last);
+        const uint32_t k3 = 2u * kRK * (s + 3u < last ? s + 3u : last);
+        rt_load(a0, a1, b0, b1, xb, wb, ao, bo, k2);
+        rt_compute(acc, lds[0], a_off, b_off);
+        rt_store(lds[1], soff, p0, p1, q0, q1);
+        __syncthreads();
+        if (s + 1u >= nsteps) break;
+        rt_load(p0, p1, q0, q1, xb, wb, ao, bo, k3);
+        rt_compute(acc, lds[1], a_off, b_off);
+        rt_store(lds[0], soff, a0, a1, b0, b1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t e = e0 + 64u * wn + 16u * (uint32_t)j + c;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t t = t0 + 32u * wm + 16u * (uint32_t)i + 4u * g + (uint32_t)r;
+                if (t < T && e < E) out[(uint64_t)t * E + e] = acc[i][j][r];
+            }
+        }
+}
+
+/* ---------------------------------------------------------------------- */
+/* certification and selection                                             */
+/* ---------------------------------------------------------------------- */
+
+struct CertArgs {
+    uint32_t *ids;
+    float *weights;
+    uint32_t *ids2;
+    float *w2;
+    const float *approx;
+    const float *norms;
+    const float *bias;
+    const uint16_t *x;
+    const uint16_t *w;
+    uint32_t T, E, H, k;
+    float scale, err_coef;
+};
+
+/* Sum over the wave of a per-lane count < 32. */
+__device__ __forceinline__ uint32_t wave_count(uint32_t v) {
+    uint32_t n = 0u;
+#pragma unroll
+    for (int b = 0; b < 5; b++) n += (uint32_t)__popcll(__ballot((v >> b) & 1u)) << b;
+    return n;
+}
+
+/* The float whose choice_key is `key` (key != 0). */
+__device__ __forceinline__ float key_value(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+constexpr uint32_t kNanBits = 0x7fc00000u;
+
+/* Scratch of one certify block (one token). */
+struct CertSmem {
+    uint4 x[64 * kTopkSlots];       /* the token's row, 8-element chunks */
+    uint32_t cand[64 * kTopkSlots]; /* candidate expert ids */
+    uint32_t logit[64 * kTopkSlots]; /* exact logit bits by expert (NaN: none) */
+    uint32_t ncand;
+    TopkWaveSmem topk;
+};
+
+/*
+ * One block of 4 waves per token. Wave 0 derives the candidate list from
+ * the approximate logits; then every wave computes the exact w64-order
+ * logits of candidates wave, wave + 4, ... (lane l takes x chunks l, l +
+ * 64, ... -- the chunks it owns in that order -- from the block's copy of
+ * the row in LDS, and the next candidate row's loads are issued before the
+ * current row's FMAs, so two rows are in flight); wave 0 turns them into
+ * keys (key 0 off the list) and runs the exact selection.
+ */
+__global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
+    __shared__ CertSmem sm;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.x;
+    const uint32_t E = A.E, H = A.H, chunks = H / 8u;
+    const uint4 *xr = (const uint4 *)(A.x + (uint64_t)t * H);
+    for (uint32_t c = threadIdx.x; c < chunks; c += 256u) sm.x[c] = xr[c];
+    __syncthreads();
+    if (wave == 0u) {
+        float la[kTopkSlots], nb[kTopkSlots], bs[kTopkSlots];
+        const float *ar = A.approx + (uint64_t)t * E;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t e = lane + 64u * (uint32_t)j;
+            const bool v = e < E;
+            la[j] = v ? ar[e] : 0.0f;
+            nb[j] = v ? A.norms[e] : 0.0f;
+            bs[j] = v ? A.bias[e] : 0.0f;
+        }
+        /* ||x_t|| (upper bound) */
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t c = lane + 64u * (uint32_t)j;
+            const uint4 v = c < chunks ? sm.x[c] : make_uint4(0u, 0u, 0u, 0u);
+            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                ss = fmaf(bf16_lo(u[q]), bf16_lo(u[q]), ss);
+                ss = fmaf(bf16_hi(u[q]), bf16_hi(u[q]), ss);
+            }
+        }
+        const float nx = __fmul_rn(__fsqrt_rn(wave_sum(ss)), kNormInflate);
+        bool fin = isfinite(nx);
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++)
+            fin = fin && isfinite(la[j]) && isfinite(nb[j]) && isfinite(bs[j]);
+        /* approximate choices and keys; the choice error bound uses the
+         * largest sigmoid slope over [a - err, a + err] */
+        uint32_t key[kTopkSlots];
+        float ch[kTopkSlots], ce[kTopkSlots];
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t e = lane + 64u * (uint32_t)j;
+            key[j] = 0u;
+            ch[j] = 0.0f;
+            ce[j] = 0.0f;
+            if (e < E) {
+                const float s = det_sigmoid(la[j]);
+                key[j] = choice_key(s, bs[j]);
+                ch[j] = __fadd_rn(s, bs[j]);
+                const float err = fmaf(__fmul_rn(A.err_coef, nb[j]), nx, 1e-30f);
+                const float m = fmaxf(0.0f, __fsub_rn(fabsf(la[j]), err));
+                const float sm_ = det_sigmoid(m);
+                const float slope = __fmul_rn(__fmul_rn(sm_, __fsub_rn(1.0f, sm_)),
+                                              1.0f + 1.0f / 1024.0f);
+                ce[j] = fmaf(slope, err, fmaf(4.76837158203125e-7f, fabsf(ch[j]), 2e-6f));
+            }
+        }
+        /* the k-th largest approximate key */
+        uint32_t thr = 0u;
+        for (int b = 31; b >= 0; b--) {
+            const uint32_t tt = thr | (1u << b);
+            uint32_t cnt = 0u;
+#pragma unroll
+            for (int j = 0; j < kTopkSlots; j++) cnt += key[j] >= tt ? 1u : 0u;
+            if (wave_count(cnt) >= A.k) thr = tt;
+        }
+        /* E_k: the largest error bound among the experts at or above it */
+        float ek = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++)
+            if (thr != 0u && key[j] >= thr) ek = fmaxf(ek, ce[j]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ek = fmaxf(ek, __shfl_xor(ek, o, 64));
+        const bool exact_all = __ballot(!fin) != 0ull || thr == 0u;
+        float lim = 0.0f;
+        if (!exact_all) {
+            lim = __fsub_rn(key_value(thr), ek);
+            lim = __fsub_rn(lim, __fmul_rn(fabsf(lim), 2.384185791015625e-7f));
+        }
+        uint32_t mine = 0u;
+        bool cand[kTopkSlots];
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t e = lane + 64u * (uint32_t)j;
+            cand[j] = e < E && (exact_all || __fadd_rn(ch[j], ce[j]) >= lim);
+            mine += cand[j] ? 1u : 0u;
+        }
+        const unsigned long long below = (1ull << lane) - 1ull;
+        uint32_t pos = 0u, ncand = 0u;
+#pragma unroll
+        for (int b = 0; b < 5; b++) {
+            const unsigned long long m = __ballot((mine >> b) & 1u);
+            pos += (uint32_t)__popcll(m & below) << b;
+            ncand += (uint32_t)__popcll(m) << b;
+        }
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t e = lane + 64u * (uint32_t)j;
+            if (cand[j]) sm.cand[pos++] = e;
+            if (e < E) sm.logit[e] = kNanBits;
+        }
+        if (lane == 0u) sm.ncand = ncand;
+    }
+    __syncthreads();
+    /* exact w64-order logits of this wave's candidates, two rows in flight */
+    const uint32_t ncand = sm.ncand;
+    auto load_row = [&](uint32_t e, uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) {
+        const uint32_t eu = (uint32_t)__builtin_amdgcn_readfirstlane((int)e); /* wave-uniform */
+        const uint4 *wr = (const uint4 *)(A.w + (uint64_t)eu * H);
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t c = lane + 64u * (uint32_t)j;
+            v[j] = wr[c < chunks ? c : chunks - 1u];
+        }
+    };
+    auto dot_row = [&](const uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) -> float {
+        float s1[1] = {0.0f};
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            if (lane + 64u * (uint32_t)j < chunks) {
+                const uint4 xq = sm.x[lane + 64u * (uint32_t)j];
+                const uint32_t xu[4] = {xq.x, xq.y, xq.z, xq.w};
+                const uint32_t a[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    s1[0] = fmaf(bf16_lo(a[q]), bf16_lo(xu[q]), s1[0]);
+                    s1[0] = fmaf(bf16_hi(a[q]), bf16_hi(xu[q]), s1[0]);
+                }
+            }
+        }
+        return wave_sum_rows<1>(s1);
+    };
+    uint4 wa[kTopkSlots], wb[kTopkSlots];
+    if (wave < ncand) load_row(sm.cand[wave], wa);
+    for (uint32_t p = wave; p < ncand; p += 8u) {
+        /* rows p (in wa) and p + 4 (into wb, issued before p's FMAs) */
+        const bool second = p + 4u < ncand;
+        if (second) load_row(sm.cand[p + 4u], wb);
+        const float l1 = dot_row(wa);
+        if (lane == 0u) sm.logit[sm.cand[p]] = __float_as_uint(l1);
+        if (!second) break;
+        if (p + 8u < ncand) load_row(sm.cand[p + 8u], wa);
+        const float l2 = dot_row(wb);
+        if (lane == 0u) sm.logit[sm.cand[p + 4u]] = __float_as_uint(l2);
+    }
+    __syncthreads();
+    if (wave != 0u) return;
+    /* exact keys (key 0 off the candidate list), then the exact selection */
+    uint32_t key[kTopkSlots];
+    float score[kTopkSlots];
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) {
+        const uint32_t e = lane + 64u * (uint32_t)j;
+        key[j] = 0u;
+        score[j] = 0.0f;
+        if (e < E) {
+            score[j] = det_sigmoid(__uint_as_float(sm.logit[e]));
+            key[j] = choice_key(score[j], A.bias[e]);
+        }
+    }
+    const uint64_t o = (uint64_t)t * A.k;
+    topk_select_wave(key, score, A.k, A.scale, A.ids + o, A.weights + o,
+                     A.ids2 ? A.ids2 + o : nullptr, A.w2 ? A.w2 + o : nullptr, sm.topk);
+}
+
+}  // namespace
+
+bool router_certified_supported(uint32_t tokens, uint32_t experts, uint32_t hidden,
+                                uint32_t top_k, const void *router_weight, const void *x) {
+    return tokens > 0u && experts >= top_k && experts <= 64u * (uint32_t)kTopkSlots &&
+           top_k >= 1u && top_k <= 32u && hidden % kRK == 0u &&
+           hidden <= 8u * 64u * (uint32_t)kTopkSlots &&
+           (((uintptr_t)router_weight | (uintptr_t)x) % 16u) == 0u;
+}
+
+bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, float *w2,
+                             float *approx, float *norms, const void *router_weight,
+                             const void *router_bias, const void *x, uint32_t T, uint32_t E,
+                             uint32_t H, uint32_t k, float scale, hipStream_t st,
+                             const StageMarker *mark) {
+    if (!router_certified_supported(T, E, H, k, router_weight, x)) return false;
+    const uint16_t *w = (const uint16_t *)router_weight;
+    hipLaunchKernelGGL(router_norms_kernel, dim3((E + 3u) / 4u), dim3(256), 0, st, norms, w, E, H);
+    const uint32_t works = ((T + kRT - 1u) / kRT) * ((E + kRT - 1u) / kRT);
+    hipLaunchKernelGGL(router_mfma_kernel, dim3(8u * ((works + 7u) / 8u)), dim3(512), 0, st,
+                       approx, (const uint16_t *)x, w, T, E, H);
+    if (mark) (*mark)(K3_MOE_STAGE_TOPK);
+    CertArgs A{ids, weights, ids2, w2, approx, norms, (const float *)router_bias,
+               (const uint16_t *)x, w, T, E, H, k, scale,
+               (float)(H / 32u + 270u) * 5.9604644775390625e-8f * (1.0f + 1.0f / 1024.0f)};
+    hipLaunchKernelGGL(router_certify_kernel, dim3(T), dim3(256), 0, st, A);
+    return hipGetLastError() == hipSuccess;
+}
+
+}  // namespace k3
+
+/* ---------------------------------------------------------------------- */
+/* C ABI                                                                   */
+/* ---------------------------------------------------------------------- */
+
+namespace {
+size_t up256(size_t n) { return (n + 255u) & ~(size_t)255u; }
+}  // namespace
+
+extern "C" size_t k3_moe_router_scratch_bytes(uint32_t token_count, uint32_t expert_count) {
+    if (token_count == 0u || token_count > 65535u || expert_count == 0u ||
+        expert_count > 64u * (uint32_t)k3::kTopkSlots)
+        return 0u;
+    return up256(4ull * token_count * expert_count) + up256(4ull * expert_count);
+}
+
+extern "C" bool k3_moe_router_bf16(uint32_t *expert_ids, float *expert_weights,
+                                   const void *hidden, const void *router_weight,
+                                   const void *router_bias, uint32_t token_count,
+                                   uint32_t expert_count, uint32_t hidden_size, uint32_t top_k,
+                                   float scaling_factor, void *scratch, size_t scratch_bytes,
+                                   void *stream) {
+    const size_t need = k3_moe_router_scratch_bytes(token_count, expert_count);
+    if (!expert_ids || !expert_weights || !hidden || !router_weight || !router_bias ||
+        !scratch || need == 0u || scratch_bytes < need || ((uintptr_t)scratch % 256u) != 0u ||
+        hidden_size == 0u || top_k == 0u || top_k > 32u || top_k > expert_count)
+        return false;
+    const hipStream_t st = (hipStream_t)stream;
+    float *logits = (float *)scratch;
+    float *norms = (float *)((uint8_t *)scratch + up256(4ull * token_count * expert_count));
+    if (token_count >= 128u &&
+        k3::router_certified_supported(token_count, expert_count, hidden_size, top_k,
+                                       router_weight, hidden))
+        return k3::launch_router_certified(expert_ids, expert_weights, nullptr, nullptr, logits,
+                                           norms, router_weight, router_bias, hidden,
+                                           token_count, expert_count, hidden_size, top_k,
+                                           scaling_factor, st, nullptr);
+    return k3::launch_bf16_rows_f32_any(logits, router_weight, hidden, token_count, expert_count,
+                                        hidden_size, st) &&
+           k3::launch_router_topk(expert_ids, expert_weights, nullptr, nullptr, logits,
+                                  (const float *)router_bias, token_count, expert_count, top_k,
+                                  scaling_factor, st);
+}

@@ -41,7 +41,7 @@ def run_and_check(cfg, T, cuda, layer=None, residual=True, precision=0):
 
 
 @pytest.mark.parametrize("kind", [N.STATIC_Q8, N.STATIC_BF16])
-@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("T", [1, 5, 160])  # 160: the certified MFMA router
 def test_native_small_bitexact(cuda, kind, T):
     cfg = N.NativeConfig(SMALL.name, T, SMALL.hidden, SMALL.latent, SMALL.experts, SMALL.top_k,
                          SMALL.ffn, SMALL.shared, static_kind=kind, seed=SMALL.seed + kind)

@@ -1,0 +1,116 @@
+"""GPU parity of the certified MFMA router (k3_moe_router_bf16) against the
+exact prefill router pair k3_rocm_bf16_gemm_f32 + k3_rocm_router_topk_f32_batch
+(k3_engine_prefill.inc:1448-1460): ids and weights bit-identical on every
+token, including exact ties, all-zero, huge, tiny and non-finite tokens."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from moonshine_amd import ops
+from moonshine_amd._lib import lib
+from moonshine_amd.synth import CONFIGS, f32_to_bf16_bits, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def exact_routes(w, b, x, T, E, H, k, scale, cuda):
+    logits = torch.empty((T, E), dtype=torch.float32, device=cuda)
+    ids = torch.empty((T, k), dtype=torch.int32, device=cuda)
+    wts = torch.empty((T, k), dtype=torch.float32, device=cuda)
+    assert ops.k3_rocm_bf16_gemm_f32(logits, w, x, T, E, H)
+    assert ops.k3_rocm_router_topk_f32_batch(ids, wts, logits, b, T, E, k, scale)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), wts.cpu().numpy(), logits.cpu().numpy()
+
+
+def certified_routes(w, b, x, T, E, H, k, scale, cuda):
+    need = lib().k3_moe_router_scratch_bytes(T, E)
+    assert need > 0
+    scratch = torch.empty(need, dtype=torch.uint8, device=cuda)
+    ids = torch.full((T, k), -7, dtype=torch.int32, device=cuda)
+    wts = torch.full((T, k), -7.0, dtype=torch.float32, device=cuda)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert lib().k3_moe_router_bf16(P(ids), P(wts), P(x), P(w), P(b), T, E, H, k, scale,
+                                    P(scratch), need,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    approx = scratch[:4 * T * E].view(torch.float32).view(T, E).cpu().numpy()
+    return ids.cpu().numpy(), wts.cpu().numpy(), approx
+
+
+def check(w_bits, bias, x_bits, k, scale, cuda, bound_rows=None):
+    T, H = x_bits.shape
+    E = w_bits.shape[0]
+    w = dev(w_bits.view(np.int16), cuda)
+    b = dev(bias.astype(np.float32), cuda)
+    x = dev(x_bits.view(np.int16), cuda)
+    want_ids, want_w, logits = exact_routes(w, b, x, T, E, H, k, scale, cuda)
+    got_ids, got_w, approx = certified_routes(w, b, x, T, E, H, k, scale, cuda)
+    np.testing.assert_array_equal(got_ids, want_ids)
+    np.testing.assert_array_equal(got_w.view(np.uint32), want_w.view(np.uint32))
+    if bound_rows is not None and T >= 128:
+        # the MFMA logits sit inside the error bound the candidates rely on:
+        # |a - l| <= (H / 32 + 270) u ||w_e|| ||x_t||, u = 2^-24 (both sums'
+        # rounding)
+        wf = (w_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        xf = (x_bits[bound_rows].astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        scale_ = np.linalg.norm(xf, axis=1)[:, None] * np.linalg.norm(wf, axis=1)[None, :]
+        diff = np.abs(approx[bound_rows].astype(np.float64) - logits[bound_rows])
+        bound = (H // 32 + 270) * 2.0 ** -24 * scale_
+        assert (diff <= bound).all(), float((diff / bound).max())
+    return got_ids
+
+
+def bf16(a):
+    return f32_to_bf16_bits(np.asarray(a, dtype=np.float32))
+
+
+def test_certified_router_k3_prefill(cuda):
+    """The cfg4 batch: 8192 tokens, 896 experts, hidden 7168, top-16."""
+    cfg = CONFIGS[4]
+    inp = make_inputs(cfg)
+    check(inp.router_weight, inp.router_bias, inp.hidden, cfg.top_k, cfg.scale, cuda,
+          bound_rows=np.arange(0, cfg.tokens, 97))
+
+
+@pytest.mark.parametrize("T,E,H,k", [(128, 64, 512, 4), (300, 200, 1024, 8), (517, 896, 7168, 16),
+                                     (1000, 1024, 8192, 32), (130, 40, 64, 1)])
+def test_certified_router_shapes(cuda, T, E, H, k):
+    rng = np.random.default_rng(T * 7 + E)
+    w = bf16(rng.normal(0, 0.02, (E, H)))
+    b = (rng.normal(0, 0.01, E)).astype(np.float32)
+    x = bf16(rng.normal(0, 1, (T, H)))
+    check(w, b, x, k, 2.5, cuda, bound_rows=np.arange(T))
+
+
+def test_certified_router_adversarial(cuda):
+    """Exact logit ties (duplicated router rows, equal biases), all-zero
+    tokens (every choice equal), huge, tiny and non-finite tokens, and a
+    bias that dominates the logits."""
+    rng = np.random.default_rng(5)
+    T, E, H, k = 256, 256, 1024, 8
+    wf = rng.normal(0, 0.02, (E, H)).astype(np.float32)
+    wf[1::2] = wf[0::2]  # rows 2j and 2j + 1 equal
+    w = bf16(wf)
+    b = np.repeat(rng.normal(0, 0.01, E // 2), 2).astype(np.float32)
+    xf = rng.normal(0, 1, (T, H)).astype(np.float32)
+    xf[0] = 0.0
+    xf[1] *= 1e30
+    xf[2] *= 1e-30
+    xf[3, 7] = np.nan
+    xf[4, 9] = np.inf
+    xf[5, 11] = -np.inf
+    xf[6] = 3e38  # logits overflow
+    xf[7] = xf[8]
+    x = bf16(xf)
+    ids = check(w, b, x, k, 1.0, cuda)
+    # ties resolved towards the lower id, like the exact router
+    assert (ids[9:] >= 0).all()
+    big_bias = rng.normal(0, 10.0, E).astype(np.float32)
+    check(w, big_bias, x, k, 1.0, cuda)

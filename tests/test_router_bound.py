@@ -1,0 +1,86 @@
+"""CPU checks of what the certified MFMA router (k3_router.hip) relies on:
+
+1. the deterministic sigmoid (the oracle's k3o_sigmoid(x, 0) evaluates the
+   device's sequence) is within 3e-7 of the real sigmoid everywhere, which
+   the 2e-6 absolute slack of the choice bound covers twice over;
+2. the candidate rule keeps every expert of the exact top-k: with exact
+   logits l, approximate logits a anywhere within |a - l| <= err, choices
+   c = sigmoid + bias, ce = s'(max(0, |a| - err)) err + 2e-6 + 2^-21 |c|,
+   T_k the k-th largest approximate choice and E_k the largest ce at or
+   above it, the exact top-k (ties towards the lower id) satisfies
+   c~ + ce >= T_k - E_k. Brute force over random and adversarial cases
+   (errors pushed to the bound against the true order, exact ties).
+"""
+import numpy as np
+
+import _oracle as O
+
+L = O.lib()
+
+
+def sig64(z):
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def test_deterministic_sigmoid_error():
+    z = np.concatenate([np.linspace(-90, 90, 400001), np.linspace(-4, 4, 100001)]).astype(np.float32)
+    got = np.array([L.k3o_sigmoid(float(v), 0) for v in z[::5]], np.float64)
+    want = sig64(z[::5].astype(np.float64))
+    assert np.abs(got - want).max() <= 3e-7
+
+
+def det_sigmoid_f32(z, rng):
+    """The real sigmoid rounded to f32, off by up to 3e-7 (the pinned bound)."""
+    s = sig64(z.astype(np.float64))
+    return (s + rng.uniform(-3e-7, 3e-7, s.shape)).astype(np.float32)
+
+
+def candidates(a, err, bias, k, rng):
+    s = det_sigmoid_f32(a, rng)
+    ch = (s + bias).astype(np.float32)
+    m = np.maximum(0.0, np.abs(a) - err).astype(np.float32)
+    sm = sig64(m.astype(np.float64))
+    slope = (sm * (1 - sm) * (1 + 2.0 ** -10)).astype(np.float32)
+    ce = (slope * err + 2e-6 + 4.76837158203125e-7 * np.abs(ch)).astype(np.float32)
+    order = np.lexsort((np.arange(len(ch)), -ch.astype(np.float64)))
+    tk = ch[order[k - 1]]
+    ek = ce[ch >= tk].max()
+    lim = np.float32(tk - ek)
+    lim = np.float32(lim - abs(lim) * 2.384185791015625e-7)
+    return (ch + ce).astype(np.float32) >= lim
+
+
+def exact_topk(l, bias, k, rng):
+    s = det_sigmoid_f32(l, rng)
+    ch = (s + bias).astype(np.float32).astype(np.float64)
+    order = np.lexsort((np.arange(len(ch)), -ch))
+    return order[:k]
+
+
+def test_candidate_rule_keeps_exact_topk():
+    rng = np.random.default_rng(11)
+    for trial in range(3000):
+        E = int(rng.choice([16, 64, 300, 896, 1024]))
+        k = int(rng.integers(1, min(E, 32) + 1))
+        spread = float(rng.choice([0.1, 1.0, 3.0, 20.0]))
+        l = rng.normal(0, spread, E).astype(np.float32)
+        if trial % 7 == 0:  # exact ties
+            l[1::2] = l[0::2][: len(l[1::2])]
+        bias = (rng.normal(0, float(rng.choice([0.0, 0.01, 0.5, 5.0])), E)).astype(np.float32)
+        if trial % 11 == 0:
+            bias[:] = bias[0]
+        err = (np.abs(rng.normal(0, 0.01, E)) * float(rng.choice([0.01, 1.0, 30.0]))).astype(np.float32)
+        # approximate logits: random within the bound, or pushed to the bound
+        # against the exact order (top experts down, the rest up)
+        if trial % 2:
+            a = l + err * rng.uniform(-1, 1, E).astype(np.float32)
+        else:
+            top = exact_topk(l, bias, k, rng)
+            sgn = np.ones(E, np.float32)
+            sgn[top] = -1.0
+            a = l + sgn * err
+        a = a.astype(np.float32)
+        cand = candidates(a, err, bias, k, rng)
+        want = exact_topk(l, bias, k, rng)
+        assert cand[want].all(), (trial, E, k)
+        assert cand.sum() >= k
