@@ -213,10 +213,10 @@ def run_native(args):
                      "traffic": None, "algorithmic_bytes": nbytes, "avg_ms": ms},
     }
     if not args.no_graph:
-        log("bench: the same steps replayed from a HIP graph (two streams) ...")
-        gms = graph_ms_per_step(torch, lambda i, st: call(i, st, 2), R, args.steps)
-        result["graph"] = {"streams": 2, "ms_per_step": gms, "value": T / (gms * 1e-3),
-                           "hbm_gbps": nbytes / (gms * 1e-3) / 1e9}
+        log("bench: the same steps replayed from a HIP graph ...")
+        gms = graph_ms_per_step(torch, lambda i, st: call(i, st, args.streams), R, args.steps)
+        result["graph"] = {"streams": args.streams, "ms_per_step": gms,
+                           "value": T / (gms * 1e-3), "hbm_gbps": nbytes / (gms * 1e-3) / 1e9}
     if not args.no_cpu_baseline and T == 1:
         log("bench: CPU baseline (composed C oracle) ...")
         sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))

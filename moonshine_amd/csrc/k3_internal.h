@@ -48,6 +48,14 @@ bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, floa
                              uint32_t H, uint32_t k, float scale, hipStream_t stream,
                              const StageMarker *mark);
 
+/* launch_q8_gateup (rows x cols) and launch_q8_gemv (out_rows x cols, no
+ * addends) on the same x as one launch; the same bits as the two calls. */
+bool launch_q8_gateup_and_gemv(uint16_t *act, const void *gate_codes, const void *gate_scales,
+                               const void *up_codes, const void *up_scales, const void *x,
+                               uint32_t rows, uint32_t cols, uint32_t kind, float beta, float lb,
+                               uint16_t *out, const void *codes, const void *scales,
+                               uint32_t out_rows, hipStream_t stream);
+
 /* Router top-k; ids2/w2 (nullable) receive extra copies (e.g. mapped host
  * memory) while ids/w stay in device memory for later kernels. */
 bool launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,

@@ -166,10 +166,24 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
         ok = hipEventRecord(ev->fork, st) == hipSuccess &&
              hipStreamWaitEvent(side, ev->fork, 0) == hipSuccess;
     }
+    /* one stream, one token, Q8-128 latent: the latent projection and the
+     * shared gate/up read the same x, so they run as one grid */
+    const bool pair = fused && !ev && W.routed_down.kind == K3_MOE_STATIC_Q8_128 &&
+                      k3::q8_gemv_fits(H, W.routed_down.data, hidden);
     /* side stream (or the main one): latent, then the shared activation */
-    ok = ok && project(W.routed_down, ws.latent, hidden, T, side);
+    if (pair) {
+        ok = ok && k3::launch_q8_gateup_and_gemv(ws.act, W.shared_gate.data,
+                                                 W.shared_gate.scales, W.shared_up.data,
+                                                 W.shared_up.scales, hidden, S, H,
+                                                 s.routed.activation, beta, lb, ws.latent,
+                                                 W.routed_down.data, W.routed_down.scales, D,
+                                                 st);
+    } else {
+        ok = ok && project(W.routed_down, ws.latent, hidden, T, side);
+    }
     if (ev) ok = ok && hipEventRecord(ev->latent, side) == hipSuccess;
-    if (fused) {
+    if (pair) {
+    } else if (fused) {
         ok = ok && k3::launch_q8_gateup(ws.act, W.shared_gate.data, W.shared_gate.scales,
                                         W.shared_up.data, W.shared_up.scales, hidden, S, H,
                                         s.routed.activation, beta, lb, side);

@@ -480,24 +480,57 @@ __device__ __forceinline__ uint32_t rms_apply2(uint32_t u, uint32_t w, float inv
 constexpr int kQ8DualRows = 8; /* rows per block of the DUAL kernel */
 
 template <bool DUAL, int R, int RS, bool NORM>
-__global__ __launch_bounds__(256) void q8_gemv_kernel(
-        uint16_t *__restrict__ out, const int8_t *__restrict__ codes_a,
-        const float *__restrict__ scales_a, const int8_t *__restrict__ codes_b,
-        const float *__restrict__ scales_b, const uint16_t *__restrict__ x, uint32_t rows,
-        uint32_t cols, uint32_t align16, const uint16_t *__restrict__ add1,
-        const uint16_t *__restrict__ add2, uint32_t act_kind, float beta, float lb,
-        const uint16_t *__restrict__ norm_w, float eps) {
+struct Q8GemvSmem {
+    static constexpr int NM = DUAL ? 2 : 1, SPS = 4 / RS, RB = R * RS;
+    float part[NM * RB][SPS][64];
+    float scl[NM * RB][SPS][64];
+    float npart[4];
+    uint4 xn[NORM ? 8192 / 8 : 1]; /* the normalised vector */
+};
+
+struct Q8GemvArgs {
+    uint16_t *out;
+    const int8_t *codes_a;
+    const float *scales_a;
+    const int8_t *codes_b;
+    const float *scales_b;
+    const uint16_t *x;
+    uint32_t rows, cols, align16;
+    const uint16_t *add1, *add2;
+    uint32_t act_kind;
+    float beta, lb;
+    const uint16_t *norm_w;
+    float eps;
+};
+
+/* Block `bid` of a q8_gemv launch (the kernel body, shared by the launches
+ * that run two projections as one grid). */
+template <bool DUAL, int R, int RS, bool NORM>
+__device__ __forceinline__ void q8_gemv_block(Q8GemvSmem<DUAL, R, RS, NORM> &sm, uint32_t bid,
+                                              const Q8GemvArgs &A) {
     static_assert(RS == 1 || RS == 2 || RS == 4, "row sets");
     static_assert(!DUAL || RS == 1, "DUAL uses one row set");
     constexpr int NM = DUAL ? 2 : 1, SPS = 4 / RS, RB = R * RS;
     static_assert(RB >= 4, "at least one row per wave in the reduction");
-    __shared__ float part[NM * RB][SPS][64];
-    __shared__ float scl[NM * RB][SPS][64];
-    __shared__ float npart[4];
-    __shared__ uint4 xn[NORM ? 8192 / 8 : 1]; /* the normalised vector */
+    auto &part = sm.part;
+    auto &scl = sm.scl;
+    auto &npart = sm.npart;
+    auto &xn = sm.xn;
+    uint16_t *__restrict__ out = A.out;
+    const int8_t *__restrict__ codes_a = A.codes_a;
+    const float *__restrict__ scales_a = A.scales_a;
+    const int8_t *__restrict__ codes_b = A.codes_b;
+    const float *__restrict__ scales_b = A.scales_b;
+    const uint16_t *__restrict__ x = A.x;
+    const uint32_t rows = A.rows, cols = A.cols, align16 = A.align16;
+    const uint16_t *__restrict__ add1 = A.add1;
+    const uint16_t *__restrict__ add2 = A.add2;
+    const uint16_t *__restrict__ norm_w = A.norm_w;
+    const uint32_t act_kind = A.act_kind;
+    const float beta = A.beta, lb = A.lb, eps = A.eps;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t set = wave / SPS, stripe = wave % SPS;
-    const uint32_t row0 = blockIdx.x * RB + set * R;
+    const uint32_t row0 = bid * RB + set * R;
     const uint32_t groups = cols / 32u, g = 64u * stripe + lane;
     const bool active = g < groups;
     /* NORM: the vector and the norm weight first, so that waiting for them
@@ -576,7 +609,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(
         p[q] = acc;
     }
     const float v = wave_sum_rows<NM * RPW>(p);
-    const uint32_t base = blockIdx.x * RB + RPW * wave;
+    const uint32_t base = bid * RB + RPW * wave;
     if constexpr (DUAL) {
         /* lanes < 32: gate rows, lanes >= 32: the same up rows */
         const float u = __shfl_xor(v, 32, 64);
@@ -595,6 +628,27 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(
             out[row] = f32_to_bf16(r);
         }
     }
+}
+
+template <bool DUAL, int R, int RS, bool NORM>
+__global__ __launch_bounds__(256) void q8_gemv_kernel(Q8GemvArgs A) {
+    __shared__ Q8GemvSmem<DUAL, R, RS, NORM> sm;
+    q8_gemv_block<DUAL, R, RS, NORM>(sm, blockIdx.x, A);
+}
+
+/* Two independent single-vector projections as one grid: blocks [0, nd)
+ * run the fused gate/up/activation (DUAL, 8 rows), the rest a plain
+ * projection (4 rows). One launch ramp and tail instead of two. */
+__global__ __launch_bounds__(256) void q8_gemv_pair_kernel(Q8GemvArgs D, Q8GemvArgs S,
+                                                           uint32_t nd) {
+    __shared__ union {
+        Q8GemvSmem<true, 8, 1, false> d;
+        Q8GemvSmem<false, 4, 1, false> s;
+    } sm;
+    if (blockIdx.x < nd)
+        q8_gemv_block<true, 8, 1, false>(sm.d, blockIdx.x, D);
+    else
+        q8_gemv_block<false, 4, 1, false>(sm.s, blockIdx.x - nd, S);
 }
 
 /* One wave per 128-element block: scale = max|w| / 127 (1 for an all-zero
@@ -1076,10 +1130,11 @@ void q8_gemv_launch(uint16_t *out, const void *codes, const void *scales, const 
                     uint32_t rows, uint32_t cols, uint32_t align16, const uint16_t *add1,
                     const uint16_t *add2, const uint16_t *norm_w, float eps, hipStream_t st) {
     constexpr uint32_t rb = R * RS;
+    const Q8GemvArgs A{out, (const int8_t *)codes, (const float *)scales, nullptr, nullptr,
+                       (const uint16_t *)x, rows, cols, align16, add1, add2, 0u, 1.0f, 1.0f,
+                       norm_w, eps};
     hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<false, R, RS, NORM>), dim3((rows + rb - 1u) / rb),
-                       dim3(256), 0, st, out, (const int8_t *)codes, (const float *)scales,
-                       nullptr, nullptr, (const uint16_t *)x, rows, cols, align16, add1, add2, 0u,
-                       1.0f, 1.0f, norm_w, eps);
+                       dim3(256), 0, st, A);
 }
 
 /* Row blocking measured on cold weights (one MI355X): 4 rows per set beats
@@ -1128,10 +1183,32 @@ bool k3::launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gat
     if (!q8_gemv_fits(cols, gate_codes, x) || !q8_gemv_fits(cols, up_codes, x) || rows == 0u)
         return false;
     const uint32_t align16 = (((uintptr_t)gate_codes | (uintptr_t)up_codes) % 16u) == 0u;
+    const Q8GemvArgs A{act, (const int8_t *)gate_codes, (const float *)gate_scales,
+                       (const int8_t *)up_codes, (const float *)up_scales, (const uint16_t *)x,
+                       rows, cols, align16, nullptr, nullptr, kind, beta, lb, nullptr, 0.0f};
     hipLaunchKernelGGL(HIP_KERNEL_NAME(q8_gemv_kernel<true, kQ8DualRows, 1, false>),
-                       dim3((rows + kQ8DualRows - 1u) / kQ8DualRows), dim3(256), 0, st, act,
-                       (const int8_t *)gate_codes, (const float *)gate_scales,
-                       (const int8_t *)up_codes, (const float *)up_scales, (const uint16_t *)x, rows,
-                       cols, align16, nullptr, nullptr, kind, beta, lb, nullptr, 0.0f);
+                       dim3((rows + kQ8DualRows - 1u) / kQ8DualRows), dim3(256), 0, st, A);
+    return hipGetLastError() == hipSuccess;
+}
+
+bool k3::launch_q8_gateup_and_gemv(uint16_t *act, const void *gate_codes,
+                                   const void *gate_scales, const void *up_codes,
+                                   const void *up_scales, const void *x, uint32_t rows,
+                                   uint32_t cols, uint32_t kind, float beta, float lb,
+                                   uint16_t *out, const void *codes, const void *scales,
+                                   uint32_t out_rows, hipStream_t st) {
+    if (!q8_gemv_fits(cols, gate_codes, x) || !q8_gemv_fits(cols, up_codes, x) ||
+        !q8_gemv_fits(cols, codes, x) || rows == 0u || out_rows == 0u)
+        return false;
+    const uint32_t a16d = (((uintptr_t)gate_codes | (uintptr_t)up_codes) % 16u) == 0u;
+    const uint32_t a16s = ((uintptr_t)codes % 16u) == 0u;
+    const Q8GemvArgs D{act, (const int8_t *)gate_codes, (const float *)gate_scales,
+                       (const int8_t *)up_codes, (const float *)up_scales, (const uint16_t *)x,
+                       rows, cols, a16d, nullptr, nullptr, kind, beta, lb, nullptr, 0.0f};
+    const Q8GemvArgs S{out, (const int8_t *)codes, (const float *)scales, nullptr, nullptr,
+                       (const uint16_t *)x, out_rows, cols, a16s, nullptr, nullptr, 0u, 1.0f,
+                       1.0f, nullptr, 0.0f};
+    const uint32_t nd = (rows + kQ8DualRows - 1u) / kQ8DualRows, ns = (out_rows + 3u) / 4u;
+    hipLaunchKernelGGL(q8_gemv_pair_kernel, dim3(nd + ns), dim3(256), 0, st, D, S, nd);
     return hipGetLastError() == hipSuccess;
 }
