@@ -118,7 +118,7 @@ bool k3_moe_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
  * Routes of a token batch, replacing the prefill router pair
  * k3_rocm_bf16_gemm_f32 + k3_rocm_router_topk_f32_batch
  * (k3_engine_prefill.inc:1448-1460) with the same ids and weights, bit for
- * bit. From 128 tokens on (hidden % 64 == 0, hidden <= 8192, expert_count
+ * bit. From 32 tokens on (hidden % 64 == 0, hidden <= 8192, expert_count
  * <= 1024, 16-byte aligned hidden and router_weight) the logits run on bf16
  * MFMA and each token recomputes in the exact order only the experts that a
  * rigorous error bound cannot rule out of its top-k; otherwise the exact

@@ -37,9 +37,13 @@ bool launch_q8_gateup(uint16_t *act, const void *gate_codes, const void *gate_sc
 
 /* Certified MFMA router for token batches (k3_router.hip): the exact
  * router's routes and weights, with the logit GEMM on bf16 MFMA. approx
- * holds T x E floats, norms E floats. mark (nullable) is called with the
+ * holds router_slice_cap(T, E) x T x E floats, norms E floats. mark (nullable) is called with the
  * top-k stage between the logits and the selection. */
 struct StageMarker;
+constexpr uint32_t kRouterMaxSlices = 16;
+constexpr uint32_t kCertifiedMinTokens = 32; /* below: the exact logits + top-k kernels */
+uint32_t router_slice_cap(uint32_t T, uint32_t E);              /* for sizing approx */
+uint32_t router_slices(uint32_t T, uint32_t E, uint32_t H);     /* <= the cap */
 bool router_certified_supported(uint32_t tokens, uint32_t experts, uint32_t hidden,
                                 uint32_t top_k, const void *router_weight, const void *x);
 bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, float *w2,

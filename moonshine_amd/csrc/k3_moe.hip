@@ -73,7 +73,9 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
         return r;
     };
     const uint64_t routes = (uint64_t)T * s.top_k;
-    w.logits = (float *)take(4ull * T * s.expert_count);
+    /* router logits; T > 1: the certified router's K-sliced approximations */
+    w.logits = (float *)take(4ull * T * s.expert_count *
+                             (T > 1u ? router_slice_cap(T, s.expert_count) : 1u));
     w.scores = (float *)take(4ull * s.expert_count);
     w.keys = (uint32_t *)take(4ull * s.expert_count);
     w.ids = (uint32_t *)take(4ull * routes);
@@ -633,7 +635,6 @@ extern "C" bool k3_moe_experts_bf16(void *output, const void *hidden, const void
 /* Routes of a token batch into ws.ids / ws.weights (and the caller's
  * copies): the certified MFMA router from kCertifiedMinTokens tokens on,
  * the exact w64 logits + top-k below that; both give the same bits. */
-static constexpr uint32_t kCertifiedMinTokens = 128;
 
 static bool route_batch(const Workspace &ws, const void *hidden, const void *router_weight,
                  const void *router_bias, const k3_moe_shape &s, uint32_t T, void *expert_ids,

@@ -42,7 +42,7 @@ NativeWorkspace carve(void *base, const k3_moe_native_shape &s, uint32_t T) {
     };
     const size_t D = s.routed.hidden, H = s.model_hidden, S = s.shared_hidden;
     const size_t E = s.routed.expert_count, k = s.routed.top_k;
-    w.logits = (float *)take(4u * T * E);
+    w.logits = (float *)take(4u * T * E * (T > 1u ? k3::router_slice_cap(T, (uint32_t)E) : 1u));
     w.norms = (float *)take(4u * E);
     w.ids = (uint32_t *)take(4u * T * k);
     w.weights = (float *)take(4u * T * k);
@@ -209,7 +209,7 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
         routes_copied = true;
     } else {
         /* token batches: the certified MFMA router (same routes) */
-        const bool cert = T >= 128u && k3::router_certified_supported(T, E, H, k,
+        const bool cert = T >= k3::kCertifiedMinTokens && k3::router_certified_supported(T, E, H, k,
                                                                        W.router_weight, hidden);
         ok = ok &&
              (cert ? k3::launch_router_certified(ws.ids, ws.weights, nullptr, nullptr, ws.logits,

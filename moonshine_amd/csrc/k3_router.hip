@@ -7,7 +7,9 @@
  *
  *   router_norms_kernel    n_e >= ||w_e|| for every router row
  *   router_mfma_kernel     approximate logits a_te = x_t . w_e (bf16 MFMA,
- *                          fp32 accumulate, any summation order)
+ *                          fp32 accumulate, any summation order; with few
+ *                          tiles, K is split over blocks and
+ *                          router_slices_sum_kernel adds the slices)
  *   router_certify_kernel  one wave per token: candidates from the
  *                          approximate logits and a rigorous error bound,
  *                          exact w64-order logits for the candidates only,
@@ -153,13 +155,17 @@ __device__ __forceinline__ void rt_compute(f32x4_t (&acc)[2][4], const RouterSta
 __global__ __launch_bounds__(512) void router_mfma_kernel(float *__restrict__ out,
                                                           const uint16_t *__restrict__ x,
                                                           const uint16_t *__restrict__ w,
-                                                          uint32_t T, uint32_t E, uint32_t H) {
+                                                          uint32_t T, uint32_t E, uint32_t H,
+                                                          uint32_t S) {
     __shared__ __attribute__((aligned(16))) RouterStage lds[2];
     const uint32_t ntt = (T + kRT - 1u) / kRT, net = (E + kRT - 1u) / kRT;
-    const uint32_t works = ntt * net, per = (works + 7u) / 8u;
-    const uint32_t L = blockIdx.x, j8 = L >> 3, wk = (L & 7u) * per + j8;
-    if (j8 >= per || wk >= works) return;
+    const uint32_t works = ntt * net * S, per = (works + 7u) / 8u;
+    const uint32_t L = blockIdx.x, j8 = L >> 3, wk0 = (L & 7u) * per + j8;
+    if (j8 >= per || wk0 >= works) return;
+    /* work = (tile, K slice), the slices of a tile together */
+    const uint32_t slice = wk0 % S, wk = wk0 / S;
     const uint32_t t0 = (wk / net) * kRT, e0 = (wk % net) * kRT;
+    out += (uint64_t)slice * T * E;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1u, g = lane >> 4, c = lane & 15u;
     /* thread tid loads 16-byte piece tid % 8 of rows tid / 8 and tid / 8 +
@@ -182,7 +188,12 @@ __global__ __launch_bounds__(512) void router_mfma_kernel(float *__restrict__ ou
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t nsteps = H / kRK, last = nsteps - 1u;
+    /* this slice's K steps [s0, s0 + nsteps) */
+    const uint32_t ksteps = H / kRK;
+    const uint32_t s0 = ksteps * slice / S, nsteps = ksteps * (slice + 1u) / S - s0;
+    const uint32_t last = nsteps - 1u;
+    xb += 2u * kRK * s0;
+    wb += 2u * kRK * s0;
     /* two register sets: step s + 2's loads are issued at the start of
      * step s, so each load has two steps of MFMAs to land. Loads and
      * stores are unconditional (steps past the end reload the last one
@@ -235,6 +246,23 @@ struct CertArgs {
     uint32_t T, E, H, k;
     float scale, err_coef;
 };
+
+/* approx[i] = sum of the S K-slice partials approx[q n + i] (fp32 adds,
+ * which the error bound counts like the adds inside a slice). */
+__global__ __launch_bounds__(256) void router_slices_sum_kernel(float *__restrict__ approx,
+                                                                uint32_t S, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * 256u) {
+        float v[kRouterMaxSlices];
+#pragma unroll
+        for (uint32_t q = 0; q < kRouterMaxSlices; q++) v[q] = q < S ? approx[q * n + i] : 0.0f;
+        float a = v[0];
+#pragma unroll
+        for (uint32_t q = 1; q < kRouterMaxSlices; q++)
+            if (q < S) a = __fadd_rn(a, v[q]);
+        approx[i] = a;
+    }
+}
 
 /* Sum over the wave of a per-lane count < 32. */
 __device__ __forceinline__ uint32_t wave_count(uint32_t v) {
@@ -438,10 +466,25 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
 
 }  // namespace
 
+/* K slices of the MFMA logits: enough (tile, slice) works to spread over
+ * the CUs when there are few tiles (about 512 works), at most 16; the
+ * approximate logits take slices x T x E floats. */
+uint32_t router_slice_cap(uint32_t T, uint32_t E) {
+    const uint32_t tiles = ((T + kRT - 1u) / kRT) * ((E + kRT - 1u) / kRT);
+    const uint32_t S = tiles ? 512u / tiles : 1u;
+    return S < 1u ? 1u : (S > kRouterMaxSlices ? kRouterMaxSlices : S);
+}
+
+/* ... and at most the K steps. */
+uint32_t router_slices(uint32_t T, uint32_t E, uint32_t H) {
+    const uint32_t S = router_slice_cap(T, E), ks = H / kRK;
+    return ks == 0u ? 1u : (S < ks ? S : ks);
+}
+
 bool router_certified_supported(uint32_t tokens, uint32_t experts, uint32_t hidden,
                                 uint32_t top_k, const void *router_weight, const void *x) {
     return tokens > 0u && experts >= top_k && experts <= 64u * (uint32_t)kTopkSlots &&
-           top_k >= 1u && top_k <= 32u && hidden % kRK == 0u &&
+           top_k >= 1u && top_k <= 32u && hidden > 0u && hidden % kRK == 0u &&
            hidden <= 8u * 64u * (uint32_t)kTopkSlots &&
            (((uintptr_t)router_weight | (uintptr_t)x) % 16u) == 0u;
 }
@@ -454,9 +497,16 @@ bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, floa
     if (!router_certified_supported(T, E, H, k, router_weight, x)) return false;
     const uint16_t *w = (const uint16_t *)router_weight;
     hipLaunchKernelGGL(router_norms_kernel, dim3((E + 3u) / 4u), dim3(256), 0, st, norms, w, E, H);
-    const uint32_t works = ((T + kRT - 1u) / kRT) * ((E + kRT - 1u) / kRT);
+    const uint32_t tiles = ((T + kRT - 1u) / kRT) * ((E + kRT - 1u) / kRT);
+    const uint32_t S = router_slices(T, E, H), works = tiles * S;
     hipLaunchKernelGGL(router_mfma_kernel, dim3(8u * ((works + 7u) / 8u)), dim3(512), 0, st,
-                       approx, (const uint16_t *)x, w, T, E, H);
+                       approx, (const uint16_t *)x, w, T, E, H, S);
+    if (S > 1u) {
+        const uint64_t n = (uint64_t)T * E;
+        const uint64_t blocks = (n + 255u) / 256u;
+        hipLaunchKernelGGL(router_slices_sum_kernel, dim3((uint32_t)(blocks < 4096u ? blocks : 4096u)),
+                           dim3(256), 0, st, approx, S, n);
+    }
     if (mark) (*mark)(K3_MOE_STAGE_TOPK);
     CertArgs A{ids, weights, ids2, w2, approx, norms, (const float *)router_bias,
                (const uint16_t *)x, w, T, E, H, k, scale,
@@ -479,7 +529,9 @@ extern "C" size_t k3_moe_router_scratch_bytes(uint32_t token_count, uint32_t exp
     if (token_count == 0u || token_count > 65535u || expert_count == 0u ||
         expert_count > 64u * (uint32_t)k3::kTopkSlots)
         return 0u;
-    return up256(4ull * token_count * expert_count) + up256(4ull * expert_count);
+    return up256(4ull * k3::router_slice_cap(token_count, expert_count) * token_count *
+                 expert_count) +
+           up256(4ull * expert_count);
 }
 
 extern "C" bool k3_moe_router_bf16(uint32_t *expert_ids, float *expert_weights,
@@ -495,8 +547,10 @@ extern "C" bool k3_moe_router_bf16(uint32_t *expert_ids, float *expert_weights,
         return false;
     const hipStream_t st = (hipStream_t)stream;
     float *logits = (float *)scratch;
-    float *norms = (float *)((uint8_t *)scratch + up256(4ull * token_count * expert_count));
-    if (token_count >= 128u &&
+    float *norms = (float *)((uint8_t *)scratch +
+                             up256(4ull * k3::router_slice_cap(token_count, expert_count) *
+                                   token_count * expert_count));
+    if (token_count >= k3::kCertifiedMinTokens &&
         k3::router_certified_supported(token_count, expert_count, hidden_size, top_k,
                                        router_weight, hidden))
         return k3::launch_router_certified(expert_ids, expert_weights, nullptr, nullptr, logits,
