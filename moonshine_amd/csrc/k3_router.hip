@@ -10,7 +10,7 @@
  *                          fp32 accumulate, any summation order; with few
  *                          tiles, K is split over blocks and
  *                          router_slices_sum_kernel adds the slices)
- *   router_certify_kernel  one wave per token: candidates from the
+ *   router_certify_kernel  one block per token: candidates from the
  *                          approximate logits and a rigorous error bound,
  *                          exact w64-order logits for the candidates only,
  *                          then the exact router's top-k on exact keys
@@ -20,24 +20,27 @@
  * a fresh block of 32 products (its C operand is zero); whatever order and
  * rounding the unit uses inside, its result is taken to be within 4 u per
  * term, 128 u sum|p_block|, of the block's real sum (a truncating or
- * block-aligned adder of fp32 width stays within 2 u per term). The H / 32
- * block results are added in fp32 on the VALU (H / 32 roundings), and the
- * exact w64 chain has <= 128 fmaf roundings per lane plus a 6-level
- * butterfly. The kernel uses err_e = (H / 32 + 270) u (1 + 2^-10) n_e
- * ||x_t||, which covers both sums' errors together, since sum|p_i| <=
- * ||w_e|| ||x_t|| (Cauchy-Schwarz). The choice is sigmoid(l) +
- * bias: the real sigmoid's slope on [a - err, a + err] is at most
- * s'(max(0, |a| - err)) (the slope falls away from 0), the deterministic
- * sigmoid is within a few ulp of the real one and the bias add rounds once,
- * so the approximate and exact choices differ by at most ce_e = s'(..)
- * err_e + 2e-6 + 2^-21 |c_e|. If T_k is the k-th largest approximate choice
- * and E_k the largest ce among the experts at or above it, those k experts
- * have exact choices >= T_k - E_k, so every expert of the exact top-k (ties
- * included) has approximate choice + ce_e >= T_k - E_k. Those are the candidates; every other expert gets key 0
- * (never selected) and the candidates get their exact keys, so
- * topk_select_wave returns what it returns on all exact keys. A token with
- * any non-finite input, approximate logit, norm or bias takes every expert
- * as a candidate (the exact router on that token).
+ * block-aligned adder of fp32 width stays within 2 u per term; the worst
+ * case measured over adversarial blocks is 8 u sum|p_block|). The H / 32
+ * block results are added in fp32 (H / 32 - 1 roundings in any order),
+ * and the exact w64 chain has <= 128 fmaf roundings per lane plus a
+ * 6-level butterfly. The kernel uses err_e = (H / 32 + 270) u (1 + 2^-10)
+ * n_e ||x_t||, which covers both sums' errors together, since sum|p_i| <=
+ * ||w_e|| ||x_t|| (Cauchy-Schwarz).
+ *
+ * The choice is sigmoid(l) + bias. The real sigmoid's slope on [a - err,
+ * a + err] is at most s'(max(0, |a| - err)) (the slope falls away from 0),
+ * the deterministic sigmoid is within 3e-7 of the real one and the bias add
+ * rounds once, so the approximate and exact choices differ by at most
+ * ce_e = s'(..) err_e + 2e-6 + 2^-21 |c_e|. If T_k is the k-th largest
+ * approximate choice and E_k the largest ce among the experts at or above
+ * it, those k experts have exact choices >= T_k - E_k, so every expert of
+ * the exact top-k (ties included) has approximate choice + ce_e >= T_k -
+ * E_k. Those are the candidates; every other expert gets key 0 (never
+ * selected) and the candidates get their exact keys, so topk_select_wave
+ * returns what it returns on all exact keys. A token with any non-finite
+ * input, approximate logit, norm or bias takes every expert as a candidate
+ * (the exact router on that token).
  */
 #include "k3_decode.h"
 #include "k3_device.h"
