@@ -271,7 +271,10 @@ size_t k3_moe_native_workspace_bytes(const k3_moe_native_shape *shape, uint32_t 
 
 /* The layer above; expert_ids/expert_weights (nullable, [T, k]) receive
  * the routes. output, x and residual rows 16-byte aligned; precision as
- * for k3_moe_forward_bf16 (it selects the expert products' arithmetic).
+ * for k3_moe_forward_bf16: it selects the expert products' arithmetic, and
+ * under the MXFP8 precisions batches of 32 or more tokens also run the
+ * static projections on bf16 MFMA (exact products, fp32 sums in another
+ * order than K3_MOE_EXACT's rows kernels).
  * shared_stream (nullable, like the reference engine's shared_stream,
  * k3_engine.cu:1668-1689) takes the latent projection and the shared
  * expert's gate/up while `stream` routes; the call joins it back with events before the shared

@@ -60,6 +60,15 @@ bool launch_q8_gateup_and_gemv(uint16_t *act, const void *gate_codes, const void
                                uint16_t *out, const void *codes, const void *scales,
                                uint32_t out_rows, hipStream_t stream);
 
+/* Static projection of a token batch on bf16 MFMA (k3_proj.hip), for the
+ * MXFP8 precisions: out [T, N] bf16 = w [N, K] . x [T, K], w Q8-128 codes
+ * with [N, K / 128] scales (q8) or bf16. Products exact; fp32 summation
+ * order differs from the exact rows kernels. */
+bool proj_mfma_supported(uint32_t tokens, uint32_t rows, uint32_t cols, bool q8,
+                         const void *weights, const void *x);
+bool launch_proj_mfma(uint16_t *out, const void *x, const void *weights, const float *scales,
+                      uint32_t T, uint32_t N, uint32_t K, bool q8, hipStream_t stream);
+
 /* Router top-k; ids2/w2 (nullable) receive extra copies (e.g. mapped host
  * memory) while ids/w stay in device memory for later kernels. */
 bool launch_router_topk(uint32_t *ids, float *w, uint32_t *ids2, float *w2,

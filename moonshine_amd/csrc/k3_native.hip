@@ -68,8 +68,18 @@ bool static_ok(const k3_moe_static_weight &w, uint32_t rows, uint32_t cols) {
 }
 
 /* out [T, rows] = w . in [T, columns] with the static weight's own kernel */
+/* Token batches (T >= 32) under the MXFP8 precisions: bf16 MFMA with the
+ * exact products and fp32 sums (k3_proj.hip); otherwise the exact rows
+ * kernels of the reference entry points. */
+constexpr uint32_t kProjMfmaMinTokens = 32;
+
 bool project(const k3_moe_static_weight &w, void *out, const void *in, uint32_t T,
-             hipStream_t st) {
+             uint32_t precision, hipStream_t st) {
+    const bool q8 = w.kind == K3_MOE_STATIC_Q8_128;
+    if (precision != K3_MOE_EXACT && T >= kProjMfmaMinTokens &&
+        k3::proj_mfma_supported(T, w.rows, w.columns, q8, w.data, in))
+        return k3::launch_proj_mfma((uint16_t *)out, in, w.data, q8 ? (const float *)w.scales : nullptr, T,
+                                    w.rows, w.columns, q8, st);
     if (w.kind == K3_MOE_STATIC_BF16)
         return k3_rocm_bf16_gemm_bf16(out, w.data, in, T, w.rows, w.columns, st);
     return k3_rocm_q8_128_gemm_bf16(out, w.data, w.scales, in, T, w.rows, w.columns, st);
@@ -179,7 +189,7 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
                                                  W.routed_down.data, W.routed_down.scales, D,
                                                  st);
     } else {
-        ok = ok && project(W.routed_down, ws.latent, hidden, T, side);
+        ok = ok && project(W.routed_down, ws.latent, hidden, T, precision, side);
     }
     if (ev) ok = ok && hipEventRecord(ev->latent, side) == hipSuccess;
     if (pair) {
@@ -188,8 +198,8 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
                                         W.shared_up.data, W.shared_up.scales, hidden, S, H,
                                         s.routed.activation, beta, lb, side);
     } else {
-        ok = ok && project(W.shared_gate, ws.gate, hidden, T, side) &&
-             project(W.shared_up, ws.up, hidden, T, side) &&
+        ok = ok && project(W.shared_gate, ws.gate, hidden, T, precision, side) &&
+             project(W.shared_up, ws.up, hidden, T, precision, side) &&
              (s.routed.activation == K3_MOE_ACT_SWIGLU
                   ? k3_rocm_swiglu_bf16(ws.act, ws.gate, ws.up, sn, side)
                   : k3_rocm_situ_bf16(ws.act, ws.gate, ws.up, sn, s.routed.beta,
@@ -235,7 +245,7 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
         ok = ok &&
              k3_rocm_rms_norm_bf16(ws.normed, ws.routed, W.routed_norm, T, D, s.norm_epsilon,
                                    st) &&
-             project(W.routed_up, ws.full, ws.normed, T, st);
+             project(W.routed_up, ws.full, ws.normed, T, precision, st);
     }
     if (ev) ok = ok && hipStreamWaitEvent(st, ev->act, 0) == hipSuccess;
     if (fused) {
@@ -243,7 +253,7 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
                                       W.shared_down.scales, ws.act, H, S, ws.full,
                                       (const uint16_t *)residual, st);
     } else {
-        ok = ok && project(W.shared_down, ws.shared, ws.act, T, st);
+        ok = ok && project(W.shared_down, ws.shared, ws.act, T, precision, st);
         const uint64_t n = (uint64_t)T * H;
         if (residual) /* output = bf16(residual + bf16(full + shared)) */
             ok = ok && k3_rocm_add_bf16(ws.sum, ws.full, ws.shared, n, st) &&

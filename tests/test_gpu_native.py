@@ -72,6 +72,21 @@ def test_native_mfma_close_to_exact(cuda):
     assert rel <= 2e-3, rel
 
 
+@pytest.mark.parametrize("kind", [N.STATIC_Q8, N.STATIC_BF16])
+def test_native_mfma_projections_close_to_exact(cuda, kind):
+    """A batch under the MXFP8 precision: the static projections run on
+    bf16 MFMA too (exact products, another fp32 summation order). Routes
+    stay exact; the output is within the MFMA precision's bound."""
+    T = 300
+    cfg = N.NativeConfig("native-proj", T, 1024, 512, 64, 4, 256, 768, static_kind=kind,
+                         seed=2100 + kind)
+    got, want, _ = run_and_check(cfg, T, cuda, precision=1)
+    gf = (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    wf = (want["output"].astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    rel = np.linalg.norm(gf - wf) / np.linalg.norm(wf)
+    assert rel <= 2e-3, rel
+
+
 @pytest.mark.parametrize("T", [1, 5])
 def test_native_shared_stream_same_bits(cuda, T):
     """The shared-stream form (latent projection and shared gate/up on a
