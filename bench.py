@@ -269,7 +269,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X; "
-              "the layer would shard by tensor-parallel F slices (see DESIGN.md)", file=sys.stderr)
+              "the layer would shard by tensor-parallel F slices (each GPU holding F / N "
+              "rows of every expert)", file=sys.stderr)
         sys.exit(2)
 
     import torch
