@@ -6,7 +6,13 @@
  * kernels) and for 8 tokens (grouped kernels), with the routes copied into
  * hipHostMalloc-mapped host memory as the reference engine reads them
  * (k3_engine.cu:623-640), and checks every output bit, id and weight
- * against the C oracle (oracle/k3moe_oracle.h). Exit status 0 = match.
+ * against the C oracle (oracle/k3moe_oracle.h). Then, as an engine's token
+ * loop does: a decode token through a chain of layers enqueued back to
+ * back on one stream (each layer's output is the next layer's input and
+ * residual; routes on the device, one synchronisation at the end, no host
+ * round trip between layers -- the sync at k3_engine.cu:1569 is not
+ * needed), and the prefill router entry point (k3_moe_router_bf16) on a
+ * 40-token batch. Exit status 0 = match.
  */
 #include <hip/hip_runtime_api.h>
 
@@ -136,6 +142,82 @@ int main(void) {
         free(got);
         free(want);
     }
+
+    /* a decode token through kLayers layers, no host sync in between */
+    enum { kLayers = 4 };
+    void *d_act[kLayers + 1];
+    uint32_t *layer_ids = NULL;
+    float *layer_w = NULL;
+    CHECK(hipHostMalloc((void **)&layer_ids, 4 * kLayers * K, hipHostMallocMapped) == hipSuccess);
+    CHECK(hipHostMalloc((void **)&layer_w, 4 * kLayers * K, hipHostMallocMapped) == hipSuccess);
+    memset(layer_ids, 0xff, 4 * kLayers * K);
+    d_act[0] = d_x;
+    for (int l = 0; l < kLayers; l++) {
+        CHECK(hipMalloc(&d_act[l + 1], 2 * (size_t)H) == hipSuccess);
+        void *ids_dev = NULL, *w_dev = NULL;
+        CHECK(hipHostGetDevicePointer(&ids_dev, layer_ids + l * K, 0) == hipSuccess);
+        CHECK(hipHostGetDevicePointer(&w_dev, layer_w + l * K, 0) == hipSuccess);
+        CHECK(k3_moe_forward_bf16(d_act[l + 1], d_act[l], d_act[l], d_w, d_b, d_table, &shape,
+                                  1u, K3_MOE_EXACT, ids_dev, w_dev, ws, ws_bytes, NULL));
+    }
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+    {
+        uint16_t cur[H], nxt[H], got[H];
+        uint32_t want_ids[K];
+        float want_w[K];
+        memcpy(cur, x, sizeof cur);
+        int chain_bad = 0;
+        for (int l = 0; l < kLayers; l++) {
+            CHECK(k3o_layer(&oshape, 1u, cur, cur, router_w, bias, host_table, NULL, NULL, NULL,
+                            0, nxt, want_ids, want_w, NULL, NULL, 0, 0) == 0);
+            chain_bad |= memcmp(layer_ids + l * K, want_ids, sizeof want_ids) != 0;
+            chain_bad |= memcmp(layer_w + l * K, want_w, sizeof want_w) != 0;
+            memcpy(cur, nxt, sizeof cur);
+        }
+        CHECK(hipMemcpy(got, d_act[kLayers], sizeof got, hipMemcpyDeviceToHost) == hipSuccess);
+        chain_bad |= memcmp(got, cur, sizeof got) != 0;
+        printf("harness: %d-layer decode chain (one stream, one sync) %s\n", kLayers,
+               chain_bad ? "DIFFER" : "match");
+        bad |= chain_bad;
+    }
+    for (int l = 1; l <= kLayers; l++) hipFree(d_act[l]);
+    hipHostFree(layer_ids);
+    hipHostFree(layer_w);
+
+    /* the prefill router entry point on a token batch (the certified MFMA
+     * form from 32 tokens on) against the oracle's logits and top-k */
+    {
+        const uint32_t T = 40u;
+        uint16_t *xb = bf16_array((size_t)T * H, 1.3f);
+        void *d_xb = dev_copy(xb, 2 * (size_t)T * H);
+        const size_t rs = k3_moe_router_scratch_bytes(T, E);
+        CHECK(rs != 0);
+        void *d_scratch = NULL, *d_rids = NULL, *d_rw = NULL;
+        CHECK(hipMalloc(&d_scratch, rs) == hipSuccess);
+        CHECK(hipMalloc(&d_rids, 4 * T * K) == hipSuccess);
+        CHECK(hipMalloc(&d_rw, 4 * T * K) == hipSuccess);
+        CHECK(k3_moe_router_bf16(d_rids, d_rw, d_xb, d_w, d_b, T, E, H, K, 2.5f, d_scratch, rs,
+                                 NULL));
+        uint32_t got_ids[40 * K], want_ids[40 * K];
+        float got_w[40 * K], want_w[40 * K];
+        float *logits = malloc(4 * (size_t)T * E);
+        CHECK(hipMemcpy(got_ids, d_rids, sizeof got_ids, hipMemcpyDeviceToHost) == hipSuccess);
+        CHECK(hipMemcpy(got_w, d_rw, sizeof got_w, hipMemcpyDeviceToHost) == hipSuccess);
+        k3o_router_logits(logits, router_w, xb, T, E, H, 0);
+        CHECK(k3o_router_topk(want_ids, want_w, logits, bias, T, E, K, 2.5f, 0) == 0);
+        const int rb = memcmp(got_ids, want_ids, sizeof got_ids) != 0 ||
+                       memcmp(got_w, want_w, sizeof got_w) != 0;
+        printf("harness: router entry point, %u tokens: ids and weights %s\n", T,
+               rb ? "DIFFER" : "match");
+        bad |= rb;
+        free(logits);
+        free(xb);
+        hipFree(d_xb);
+        hipFree(d_scratch);
+        hipFree(d_rids);
+        hipFree(d_rw);
+    }
+
     hipHostFree(ids_map);
     hipHostFree(w_map);
     hipFree(ws);

@@ -382,7 +382,8 @@ def test_unaligned_expert_tensors(cuda):
 def test_c_harness():
     """The C caller of the ABI (tests/c/k3_moe_harness.c): decode and
     batched layers through k3_moe_forward_bf16 from C, routes into mapped
-    host memory, bit-exact against the C oracle."""
+    host memory, a 4-layer decode chain on one stream with one sync, and
+    the prefill router entry point, bit-exact against the C oracle."""
     import pathlib
     import subprocess
     exe = pathlib.Path(__file__).resolve().parent / "c" / "k3_moe_harness"
@@ -391,3 +392,5 @@ def test_c_harness():
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.count("output match, ids match, weights match") == 2
+    assert "4-layer decode chain (one stream, one sync) match" in r.stdout
+    assert "router entry point, 40 tokens: ids and weights match" in r.stdout
