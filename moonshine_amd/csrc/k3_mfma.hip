@@ -822,14 +822,19 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
 }
 
 /* Tile classes (rows per tile): 16, 64, 128. One-term class 0 computes
- * 32 rows so that its A chunks still split over four waves. */
+ * 32 rows so that its A chunks still split over the waves. Class 0's
+ * gate/up takes 128-row weight blocks of two waves (80 KB of LDS: two
+ * blocks per CU; cfg2 gate/up 1.68 -> 1.60 ms, cfg3 level); its down keeps
+ * 256-row blocks of four waves (measured 3% faster there). */
 template <int TERMS>
 using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2>;
 template <int TERMS>
+using Cls0G = TileCfg<1, 2, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2>;
+template <int TERMS>
 using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2>;
-/* 128 x 512 blocks: four waves, one per SIMD, each 64 activation rows x
- * 256 weight rows (accumulators in AGPRs); halves the activation re-reads
- * of a 256-wide block, two stage buffers */
+/* 128 x 512 blocks: eight waves, two per SIMD, each 64 activation rows x
+ * 128 weight rows; halves the activation re-reads of a 256-wide block, two
+ * stage buffers */
 template <int TERMS>
 using Cls2 = TileCfg<2, 4, 4, 8, TERMS, 2>;
 
@@ -870,7 +875,7 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         if (!B.tile_cap[c]) continue;
         ga.tiles = tl[c];
         ga.tile_count = B.tile_count + c;
-        if (c == 0) launch_gateup<Cls0<TERMS>>(ga, B.tile_cap[c], st);
+        if (c == 0) launch_gateup<Cls0G<TERMS>>(ga, B.tile_cap[c], st);
         if (c == 1) launch_gateup<Cls1<TERMS>>(ga, B.tile_cap[c], st);
         if (c == 2) launch_gateup<Cls2<TERMS>>(ga, B.tile_cap[c], st);
     }
