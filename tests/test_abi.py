@@ -66,6 +66,29 @@ def test_workspace_sizes_and_validation():
     assert not L.k3_moe_mx8_quantize_bf16(None, None, None, None, None, 32, None)
 
 
+def test_router_scratch_sizes_and_validation():
+    """k3_moe_router_bf16: scratch sized for the K-sliced approximate logits
+    of small batches (at most 16 slices, about 512 tile-slice works), one
+    slice at large batches; bad arguments return false before any launch."""
+    L = _lib.lib()
+    T, E = 8192, 896
+    big = L.k3_moe_router_scratch_bytes(T, E)
+    assert big >= 4 * T * E + 4 * E and big < 2 * 4 * T * E  # one slice at T = 8192
+    small = L.k3_moe_router_scratch_bytes(64, E)
+    assert small >= 16 * 4 * 64 * E  # 7 tiles: 16 slices
+    assert L.k3_moe_router_scratch_bytes(0, E) == 0
+    assert L.k3_moe_router_scratch_bytes(65536, E) == 0
+    assert L.k3_moe_router_scratch_bytes(64, 1025) == 0
+    p = ctypes.c_void_p(256)  # never dereferenced: the checks fail first
+    assert not L.k3_moe_router_bf16(p, p, p, p, p, 64, E, 7168, 16, 1.0, p, small - 1, None)
+    assert not L.k3_moe_router_bf16(p, p, p, p, p, 64, E, 7168, 33, 1.0, p, small, None)
+    assert not L.k3_moe_router_bf16(p, p, p, p, p, 64, E, 0, 16, 1.0, p, small, None)
+    assert not L.k3_moe_router_bf16(p, p, p, p, p, 64, 8, 7168, 16, 1.0, p, small, None)
+    assert not L.k3_moe_router_bf16(None, p, p, p, p, 64, E, 7168, 16, 1.0, p, small, None)
+    assert not L.k3_moe_router_bf16(p, p, p, p, p, 64, E, 7168, 16, 1.0,
+                                    ctypes.c_void_p(264), small, None)  # scratch not 256-aligned
+
+
 def test_row_alignment_is_validated_before_launch():
     """output / hidden / residual rows move 16 bytes at a time: a pointer
     that is not 16-byte aligned is refused (false, nothing launched)."""
