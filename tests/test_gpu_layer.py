@@ -299,7 +299,7 @@ class MappedHost:
         self.hip.hipHostFree(self.host)
 
 
-@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("T", [1, 5, 40])  # 40: the certified MFMA router
 def test_routes_into_mapped_host_memory(cuda, T):
     """The layer's optional route copies written straight into host-mapped
     memory, as the reference engine reads them."""

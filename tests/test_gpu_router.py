@@ -81,7 +81,8 @@ def test_certified_router_k3_prefill(cuda):
 
 @pytest.mark.parametrize("T,E,H,k", [(128, 64, 512, 4), (300, 200, 1024, 8), (517, 896, 7168, 16),
                                      (1000, 1024, 8192, 32), (130, 40, 64, 1), (33, 896, 7168, 16),
-                                     (64, 256, 2048, 8), (31, 64, 512, 4)])
+                                     (64, 256, 2048, 8), (31, 64, 512, 4), (129, 896, 7168, 16),
+                                     (257, 1000, 1024, 8)])
 def test_certified_router_shapes(cuda, T, E, H, k):
     rng = np.random.default_rng(T * 7 + E)
     w = bf16(rng.normal(0, 0.02, (E, H)))
