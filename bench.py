@@ -111,33 +111,47 @@ def recorded_traffic(workload, T, precision):
     return rec["bytes"] if rec else None
 
 
-def cpu_baseline(cfg, inputs_cpu, store, budget_s, threads):
+def cpu_threads():
+    """Every core this process may run on (sched_getaffinity)."""
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(cfg, inputs_cpu, store, budget_s, threads, full_tokens):
+    """The C oracle of the same layer (router, top-k, every route's MXFP4
+    gate/up/down and activation, combine, residual) on this host's cores,
+    OpenMP over (route, 64-row block) work items, token by token through a
+    bounded sample of the workload's own tokens. Returns tok/s; for a
+    batch larger than the sample the figure is extrapolated (the port does
+    the same work per token at any batch size: it reuses no weights)."""
     sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
     import _oracle as O  # CPU checker / baseline only
     logits = O.router_logits(inputs_cpu.router_weight, inputs_cpu.hidden)
     ids, _ = O.router_topk(logits, inputs_cpu.router_bias, cfg.top_k, cfg.scale)
     T = inputs_cpu.hidden.shape[0]
-    done = 0
     experts = {}
     t0 = time.perf_counter()
-    while done < T and time.perf_counter() - t0 < budget_s:
-        for e in ids[done]:
-            if int(e) not in experts:
-                experts[int(e)] = store.host_expert(int(e))
-        done += 1
-    gen_s = time.perf_counter() - t0
+    for e in np.unique(ids):
+        experts[int(e)] = [t.cpu().numpy() for t in store.device_expert(int(e))]
+    copy_s = time.perf_counter() - t0
+    O.layer(cfg, inputs_cpu, experts, tokens=[0], threads=threads)  # warm-up
     t0 = time.perf_counter()
     n = 0
-    while n < done:
+    while n < T:
         O.layer(cfg, inputs_cpu, experts, tokens=[n], threads=threads)
         n += 1
         if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+    rate = n / dt
+    extrap = full_tokens > n
+    return {"value": rate, "unit": "tok/s", "cores": threads, "kind": "port",
+            "extrapolated": extrap,
             "sample": f"{n} token(s) of {cfg.name} through the C oracle (router, top-k, "
-                      f"{cfg.top_k} MXFP4 experts, combine) with OpenMP over (token, expert) "
-                      f"jobs; {dt:.1f} s (+{gen_s:.1f} s regenerating experts, untimed)"}
+                      f"{cfg.top_k} MXFP4 experts, activation, combine, residual), OpenMP over "
+                      f"(route, 64-row block) on {threads} cores; {dt:.1f} s"
+                      + (f"; the full {full_tokens}-token batch extrapolates to "
+                         f"{full_tokens / rate:.0f} s" if extrap else "")
+                      + f" (+{copy_s:.1f} s copying {len(experts)} experts to the host, untimed)"}
 
 
 def run_native(args):
@@ -227,7 +241,7 @@ def run_native(args):
         logits = O.router_logits(layer.router_weight_bits, x0)
         sel, _ = O.router_topk(logits, layer.router_bias, cfg.top_k, cfg.scale)
         experts = {int(e): layer.store.host_expert(int(e)) for e in np.unique(sel)}
-        threads = min(len(os.sched_getaffinity(0)), 16)
+        threads = cpu_threads()
         n, t0 = 0, time.perf_counter()
         while n == 0 or time.perf_counter() - t0 < args.cpu_budget:
             O.native_layer(cfg, layer.router_weight_bits, layer.router_bias, layer.norm_bits,
@@ -255,6 +269,11 @@ def main():
                          "T = 1, so consecutive steps route to different experts and no step "
                          "finds its weights in the 256 MB last-level cache; 1 for T > 1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="with the default config 1: skip the batched/prefill lines (configs "
+                         "2-4 on the MFMA path, `prefill` in the JSON line)")
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--prefill-cpu-budget", type=float, default=6.0)
     ap.add_argument("--native", action="store_true",
                     help="the K3-native layer (Q8-128 static projections around the routed "
                          "experts, shared expert) instead of a BASELINE config")
@@ -290,14 +309,39 @@ def main():
         return
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from moonshine_amd import layer as L
-    from moonshine_amd._lib import STAGES, K3MoeProfile, lib
-    from moonshine_amd.synth import CONFIGS, make_inputs
+    from moonshine_amd.synth import CONFIGS
 
     cfg = CONFIGS[args.config]
     T = args.tokens or cfg.tokens
+    result = run_layer(args, cfg, T, args.precision, args.steps, args.warmup,
+                       args.rotate or (16 if T == 1 else 1), not args.no_cpu_baseline)
+    if not args.no_prefill and args.config == 1 and not args.tokens:
+        # the metric's other halves: batched decode, 512 and 8K prefill on
+        # the grouped scaled-MFMA path (two-term MXFP8 activations)
+        result["prefill"] = {}
+        for ci in (2, 3, 4):
+            pc = CONFIGS[ci]
+            r = run_layer(args, pc, pc.tokens, 1, args.prefill_steps, min(args.warmup, 3), 1,
+                          not args.no_cpu_baseline, cpu_budget=args.prefill_cpu_budget)
+            keep = ("value", "unit", "ms_per_step", "config", "layer", "roofline",
+                    "cpu_baseline")
+            result["prefill"][pc.name] = {k: r[k] for k in keep if k in r}
+            result["prefill"][pc.name]["steps"] = args.prefill_steps
+    print(json.dumps(result), flush=True)
+
+
+def run_layer(args, cfg, T, precision, steps, warmup, R, with_cpu, cpu_budget=None):
+    """k3_moe_forward_bf16 on one configuration: a fresh resident expert
+    store, R distinct token batches cycled through the steps, `steps`
+    timed calls (wall clock, synchronised on both sides), then the same
+    steps again with HIP events at the stage boundaries."""
+    import torch
+    from moonshine_amd import layer as L
+    from moonshine_amd._lib import STAGES, K3MoeProfile, lib
+    from moonshine_amd.synth import make_inputs
+
     log(f"bench: {cfg.name} T={T} building resident expert store ...")
-    R = args.rotate or (16 if T == 1 else 1)
+    torch.cuda.empty_cache()
     inputs = make_inputs(cfg, tokens=T * R)
     moe = L.build_layer(cfg, inputs, device="cuda")
     xs = L.bf16_tensor(inputs.hidden).view(R, T, cfg.hidden)
@@ -309,13 +353,13 @@ def main():
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream().cuda_stream
     hip = Hip()
-    profiles = [K3MoeProfile() for _ in range(args.steps)]
+    profiles = [K3MoeProfile() for _ in range(steps)]
     for p in profiles:
         for i in range(len(STAGES)):
             p.stage_events[i] = hip.event().value
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     argvs = [[P(out), P(xs[i]), P(rs[i]), P(moe.router_weight), P(moe.router_bias),
-              P(moe.store.table), ctypes.byref(moe.shape), T, args.precision, P(ids), P(wts),
+              P(moe.store.table), ctypes.byref(moe.shape), T, precision, P(ids), P(wts),
               P(ws), ws.numel()] for i in range(R)]
     unique_per_batch = []
 
@@ -324,26 +368,26 @@ def main():
                                                   ctypes.c_void_p(stream)):
             raise RuntimeError("k3_moe_forward_profiled_bf16 failed")
 
-    log(f"bench: warmup {args.warmup} ({R} distinct token batches) ...")
-    for i in range(max(args.warmup, R)):
+    log(f"bench: warmup {warmup} ({R} distinct token batches) ...")
+    for i in range(max(warmup, R)):
         step(i, None)
         if i < R:
             torch.cuda.synchronize()
             unique_per_batch.append(int(np.unique(ids.cpu().numpy()).size))
     torch.cuda.synchronize()
-    log(f"bench: timing {args.steps} steps ...")
+    log(f"bench: timing {steps} steps ...")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         step(i, None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = wall / args.steps * 1e3
+    ms_per_step = wall / steps * 1e3
     # second pass: the same steps with HIP events at the stage boundaries
     # (each event record adds a few microseconds, so this pass only
     # apportions time; `value` comes from the event-free pass above)
-    log(f"bench: {args.steps} profiled steps ...")
-    for i in range(args.steps):
+    log(f"bench: {steps} profiled steps ...")
+    for i in range(steps):
         step(i, ctypes.byref(profiles[i]))
     torch.cuda.synchronize()
 
@@ -354,7 +398,7 @@ def main():
         def gcall(i, st):
             if not lib().k3_moe_forward_profiled_bf16(*argvs[i % R], None, ctypes.c_void_p(st)):
                 raise RuntimeError("k3_moe_forward_profiled_bf16 failed")
-        gms = graph_ms_per_step(torch, gcall, R, args.steps)
+        gms = graph_ms_per_step(torch, gcall, R, steps)
         graph = {"ms_per_step": gms, "value": T / (gms * 1e-3)}
 
     stage_ms = {s: 0.0 for s in STAGES[:-1]}
@@ -362,16 +406,16 @@ def main():
     for p in profiles:
         ev = list(p.stage_events)
         for i, s in enumerate(STAGES[:-1]):
-            stage_ms[s] += hip.elapsed_ms(ev[i], ev[i + 1]) / args.steps
-        gpu_ms += hip.elapsed_ms(ev[0], ev[-1]) / args.steps
+            stage_ms[s] += hip.elapsed_ms(ev[i], ev[i + 1]) / steps
+        gpu_ms += hip.elapsed_ms(ev[0], ev[-1]) / steps
 
     # steps cycle through the R batches: the mean over them is each step's work
-    unique = float(np.mean([unique_per_batch[i % R] for i in range(args.steps)]))
+    unique = float(np.mean([unique_per_batch[i % R] for i in range(steps)]))
     total_bytes = algorithmic_bytes(cfg, T, unique)
     flops = T * cfg.top_k * 2 * 3 * cfg.ffn * cfg.hidden
     kms = stage_ms["gate_up"]
     layer_gbps = total_bytes / (ms_per_step * 1e-3) / 1e9
-    traffic = recorded_traffic(cfg.name, T, args.precision)
+    traffic = recorded_traffic(cfg.name, T, precision)
     if T == 1:
         kbytes = gate_up_bytes(cfg, T, unique)
         achieved = kbytes / (kms * 1e-3) / 1e9
@@ -385,20 +429,21 @@ def main():
         # the fp8 rate of the mixed fp8 x fp4 instruction actually issued
         kflops = T * cfg.top_k * 2 * 2 * cfg.ffn * cfg.hidden
         achieved = kflops / (kms * 1e-3) / 1e12
-        terms = 2 if args.precision == 1 else 1
+        terms = 2 if precision == 1 else 1
         roofline = {"kernel": "gateup_mfma_kernel", "bound": "mfma", "achieved": achieved,
                     "peak": MXFP4_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": achieved / MXFP4_PEAK_TFLOPS, "traffic": traffic,
                     "algorithmic_flops": kflops, "avg_ms": kms,
                     "mfma_terms": terms,
-                    "fp8_instr_frac": achieved * terms / FP8_PEAK_TFLOPS}
+                    "fp8_instr_frac": achieved * terms / FP8_PEAK_TFLOPS,
+                    "gate_up_hbm_gbps": gate_up_bytes(cfg, T, unique) / (kms * 1e-3) / 1e9}
     result = {
         "metric": "routed-MoE layer tok/s; decode HBM GB/s; 8K-prefill MXFP4 TFLOP/s",
         "value": T / (ms_per_step * 1e-3),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -408,25 +453,26 @@ def main():
         "config": {"workload": cfg.name, "tokens": T, "hidden": cfg.hidden,
                    "experts": cfg.experts, "top_k": cfg.top_k, "ffn": cfg.ffn,
                    "activation": "swiglu" if cfg.activation == 1 else "situ",
-                   "scale": cfg.scale, "precision": ["exact", "mx8", "mx8-1term"][args.precision],
+                   "scale": cfg.scale, "precision": ["exact", "mx8", "mx8-1term"][precision],
                    "unique_experts": unique, "distinct_batches": R},
         "layer": {"bytes": total_bytes, "hbm_gbps": layer_gbps,
-                  "hbm_frac": layer_gbps / HBM_PEAK_GBPS, "tflops": flops / (ms_per_step * 1e-3) / 1e12,
+                  "hbm_frac": layer_gbps / HBM_PEAK_GBPS,
+                  "tflops": flops / (ms_per_step * 1e-3) / 1e12,
+                  "mxfp4_frac": flops / (ms_per_step * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS,
                   "gpu_ms_events": gpu_ms, "stage_ms": stage_ms},
         "roofline": roofline,
     }
     if graph:
         result["graph"] = graph
-    if not args.no_cpu_baseline:
-        log("bench: CPU baseline (C oracle) ...")
-        threads = min(len(os.sched_getaffinity(0)), 16)
-        # a bounded sample of the same workload: up to 64 tokens (the first
-        # rows of the seeded batch; for T = 1 the rotated decode tokens),
-        # each run through the oracle layer as its own token
-        cpu_inputs = make_inputs(cfg, tokens=64)
-        result["cpu_baseline"] = cpu_baseline(cfg, cpu_inputs, moe.store, args.cpu_budget,
-                                              threads)
-    print(json.dumps(result), flush=True)
+    if with_cpu:
+        log(f"bench: CPU baseline (C oracle) for {cfg.name} ...")
+        # a bounded sample of the same workload: its first tokens (for T = 1
+        # the rotated decode tokens), each run through the oracle layer
+        cpu_inputs = make_inputs(cfg, tokens=min(64, max(T * R, 1)) if T > 1 else R)
+        result["cpu_baseline"] = cpu_baseline(
+            cfg, cpu_inputs, moe.store, cpu_budget or args.cpu_budget, cpu_threads(), T)
+    del moe, xs, rs, out, ws
+    return result
 
 
 if __name__ == "__main__":

@@ -115,6 +115,18 @@ bool k3_moe_route_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique,
                        size_t scratch_bytes, void *stream);
 
 /*
+ * The router's choice values, the quantity the top-k orders experts by:
+ * choices[t, e] = sigmoid(logits[t, e]) + bias[e] for t < token_count, e <
+ * expert_count, with the sigmoid evaluated exactly as the reference's
+ * router kernel evaluates it (k3_rocm_ops.cu:1386 under its fast-math
+ * build); bias may be NULL (the choice is then the sigmoid itself). For
+ * inspecting routing margins (how close a token is to swapping experts).
+ * token_count * expert_count must fit the grid (< 2^40).
+ */
+bool k3_moe_router_choices_f32(float *choices, const float *logits, const float *bias,
+                               uint32_t token_count, uint32_t expert_count, void *stream);
+
+/*
  * Routes of a token batch, replacing the prefill router pair
  * k3_rocm_bf16_gemm_f32 + k3_rocm_router_topk_f32_batch
  * (k3_engine_prefill.inc:1448-1460) with the same ids and weights, bit for

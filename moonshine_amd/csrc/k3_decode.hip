@@ -100,10 +100,9 @@ __global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
     if (lane < (two ? 2u : 1u)) {
         const uint32_t row = row0 + lane;
         const float v = lane ? vb : va;
-        const float score = det_sigmoid(v);
         P.logits[row] = v;
-        P.scores[row] = score;
-        P.keys[row] = choice_key(score, P.router_bias[row]);
+        P.scores[row] = det_sigmoid(v);
+        P.keys[row] = choice_key(router_sigmoid(v), P.router_bias[row]);
     }
 }
 

@@ -113,6 +113,28 @@ __device__ __forceinline__ float det_sigmoid(float x) {
     return __fdiv_rn(1.0f, __fadd_rn(1.0f, det_expf(-x)));
 }
 
+/*
+ * The router's choice sigmoid, evaluated with exactly the operations the
+ * reference's score = 1.0f / (1.0f + expf(-logit)) (k3_rocm_ops.cu:1386)
+ * becomes for gfx950 under its -ffast-math -fno-finite-math-only build:
+ * t = -logit * log2(e) rounded to fp32, e = v_exp_f32(t) (2^t), 1 + e
+ * rounded, v_rcp_f32; for logit > 87.33654 (where 2^t would be subnormal)
+ * the input is first lowered by 64 and e scaled back by e^-64 (0x114b4ea4).
+ * The expert ids depend on these bits (choice = score + bias): the same
+ * instructions give the reference's ids bit for bit, including its
+ * near-ties. v_exp_f32 and v_rcp_f32 are within 1 ulp; the result is
+ * within 3e-7 of the real sigmoid (pinned by an exhaustive sweep on the
+ * part). Route weights use det_sigmoid instead (pinned bit for bit by the
+ * CPU oracle; within 1e-6 of the reference's weights).
+ */
+__device__ __forceinline__ float router_sigmoid(float x) {
+    const bool big = x > __uint_as_float(0x42aeac50u);          /* 87.33654 */
+    const float t = big ? __fadd_rn(x, -64.0f) : x;
+    float e = __builtin_amdgcn_exp2f(__fmul_rn(t, __uint_as_float(0xbfb8aa3bu)));  /* -log2 e */
+    if (big) e = __fmul_rn(e, __uint_as_float(0x114b4ea4u));   /* e^-64 */
+    return __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e));
+}
+
 /* Gated activations on bf16-rounded gate/up values. kind 0 = SiTU(beta, lb)
  * (k3_rocm_ops.cu:66-83), kind 1 = SwiGLU g*sigmoid(g)*u. */
 __device__ __forceinline__ float gated_act(float g, float u, uint32_t kind,

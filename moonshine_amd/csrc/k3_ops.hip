@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
         score[j] = 0.0f;
         if (e < experts) {
             score[j] = det_sigmoid(lg[e]);
-            key[j] = choice_key(score[j], bias[e]);
+            key[j] = choice_key(router_sigmoid(lg[e]), bias[e]);
         }
     }
     const uint64_t o = (uint64_t)t * top_k;

@@ -30,8 +30,8 @@
  *
  * The choice is sigmoid(l) + bias. The real sigmoid's slope on [a - err,
  * a + err] is at most s'(max(0, |a| - err)) (the slope falls away from 0),
- * the deterministic sigmoid is within 3e-7 of the real one and the bias add
- * rounds once, so the approximate and exact choices differ by at most
+ * the router sigmoid (router_sigmoid, the hardware exp2/reciprocal sequence)
+ * is within 3e-7 of the real one and the bias add rounds once, so the approximate and exact choices differ by at most
  * ce_e = s'(..) err_e + 2e-6 + 2^-21 |c_e|. If T_k is the k-th largest
  * approximate choice and E_k the largest ce among the experts at or above
  * it, those k experts have exact choices >= T_k - E_k, so every expert of
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
             ch[j] = 0.0f;
             ce[j] = 0.0f;
             if (e < E) {
-                const float s = det_sigmoid(la[j]);
+                const float s = router_sigmoid(la[j]);
                 key[j] = choice_key(s, bs[j]);
                 ch[j] = __fadd_rn(s, bs[j]);
                 const float err = fmaf(__fmul_rn(A.err_coef, nb[j]), nx, 1e-30f);
@@ -458,8 +458,9 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
         key[j] = 0u;
         score[j] = 0.0f;
         if (e < E) {
-            score[j] = det_sigmoid(__uint_as_float(sm.logit[e]));
-            key[j] = choice_key(score[j], A.bias[e]);
+            const float l = __uint_as_float(sm.logit[e]);
+            score[j] = det_sigmoid(l);
+            key[j] = choice_key(router_sigmoid(l), A.bias[e]);
         }
     }
     const uint64_t o = (uint64_t)t * A.k;
@@ -565,4 +566,26 @@ extern "C" bool k3_moe_router_bf16(uint32_t *expert_ids, float *expert_weights,
            k3::launch_router_topk(expert_ids, expert_weights, nullptr, nullptr, logits,
                                   (const float *)router_bias, token_count, expert_count, top_k,
                                   scaling_factor, st);
+}
+
+/* choices[t, e] = router_sigmoid(logits[t, e]) + bias[e] (bias may be NULL). */
+__global__ __launch_bounds__(256) void router_choices_kernel(float *__restrict__ out,
+                                                             const float *__restrict__ logits,
+                                                             const float *__restrict__ bias,
+                                                             uint64_t n, uint32_t experts) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    const float s = k3::router_sigmoid(logits[i]);
+    out[i] = bias ? __fadd_rn(s, bias[i % experts]) : s;
+}
+
+extern "C" bool k3_moe_router_choices_f32(float *choices, const float *logits, const float *bias,
+                                          uint32_t token_count, uint32_t expert_count,
+                                          void *stream) {
+    if (!choices || !logits || token_count == 0u || expert_count == 0u) return false;
+    const uint64_t n = (uint64_t)token_count * expert_count;
+    if ((n + 255u) / 256u > 0xffffffffull) return false;
+    hipLaunchKernelGGL(router_choices_kernel, dim3((unsigned)((n + 255u) / 256u)), dim3(256), 0,
+                       (hipStream_t)stream, choices, logits, bias, n, expert_count);
+    return hipGetLastError() == hipSuccess;
 }

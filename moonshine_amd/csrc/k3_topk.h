@@ -1,11 +1,13 @@
 /*
  * Router top-k selection by one wavefront.
  *
- * Semantics (k3_rocm_ops.cu:1361-1450): score = sigmoid(logit), choice =
- * score + bias; experts are ordered by (choice desc, id asc) -- the order of
- * the reference's bitonic sort read from its end -- and the first top_k are
- * returned in that order with weight_r = score_r / (1e-20 + sum of the
- * selected scores in rank order) * scale. NaN choices are never selected;
+ * Semantics (k3_rocm_ops.cu:1361-1450): choice = sigmoid(logit) + bias,
+ * with the sigmoid evaluated as the reference kernel evaluates it
+ * (router_sigmoid, k3_device.h); experts are ordered by (choice desc, id
+ * asc) -- the order of the reference's bitonic sort read from its end --
+ * and the first top_k are returned in that order with weight_r = score_r /
+ * (1e-20 + sum of the selected scores in rank order) * scale, where score
+ * is the deterministic sigmoid det_sigmoid (callers pass keys and scores). NaN choices are never selected;
  * missing slots (fewer than top_k selectable experts) get id UINT32_MAX and
  * weight 0.
  *

@@ -102,6 +102,26 @@ float k3o_sigmoid(float x, int use_libm) {
     return 1.0f / (1.0f + (use_libm ? expf(-x) : k3o_expf(-x)));
 }
 
+/*
+ * The router's choice sigmoid: the reference's 1/(1 + expf(-x))
+ * (k3_rocm_ops.cu:1386) as its -ffast-math build evaluates it on gfx950
+ * (t = x * -log2(e) in fp32, 2^t, 1 + 2^t, reciprocal; inputs above
+ * 87.33654 lowered by 64 first and 2^t scaled back by e^-64). The device
+ * uses the hardware exp2 and reciprocal instructions, which are within 1 ulp
+ * but not correctly rounded; this restatement rounds both correctly (fp64
+ * then fp32), so it equals the device except where an instruction is off
+ * by its ulp (measured on the part: about 1 in 70 exp2 and 1 in 9
+ * reciprocal inputs). Choices, and therefore ids, agree except at near-ties
+ * within those ulps; the route weights use k3o_sigmoid(x, 0), bit-exact.
+ */
+float k3o_router_sigmoid(float x) {
+    const int big = x > u2f(0x42aeac50u);                 /* 87.33654 */
+    const float t = big ? x + -64.0f : x;
+    float e = (float)exp2((double)(t * u2f(0xbfb8aa3bu))); /* -log2 e */
+    if (big) e = e * u2f(0x114b4ea4u);                    /* e^-64 */
+    return (float)(1.0 / (double)(1.0f + e));
+}
+
 /* ------------------------------------------------------------------------ */
 /* activations                                                               */
 /* ------------------------------------------------------------------------ */
@@ -231,9 +251,12 @@ void k3o_bf16_gemm_f32(float *out, const uint16_t *weights,
 
 /*
  * k3_rocm_ops.cu:1361-1450 restated as the insertion-sort oracle of
- * tests/test_k3_moe_smoke.cu:215-253: score = sigmoid(logit); choice =
- * score + bias; order (choice desc, id asc); weight_r = score_r /
- * (1e-20 + sum of the k selected scores in rank order) * scale.
+ * tests/test_k3_moe_smoke.cu:215-253: choice = sigmoid(logit) + bias;
+ * order (choice desc, id asc); weight_r = score_r / (1e-20 + sum of the k
+ * selected scores in rank order) * scale with score = sigmoid(logit).
+ * use_libm = 0 (the device model): the choice sigmoid is
+ * k3o_router_sigmoid, the score sigmoid k3o_sigmoid(x, 0); use_libm = 1
+ * (the reference's CPU oracle): glibc expf for both.
  */
 int k3o_router_topk(uint32_t *ids, float *weights, const float *logits,
                     const float *bias, uint32_t tokens, uint32_t experts,
@@ -248,7 +271,7 @@ int k3o_router_topk(uint32_t *ids, float *weights, const float *logits,
         const float *lg = logits + (uint64_t)t * experts;
         for (uint32_t e = 0; e < experts; e++) {
             const float s = k3o_sigmoid(lg[e], use_libm);
-            const float c = s + bias[e];
+            const float c = (use_libm ? s : k3o_router_sigmoid(lg[e])) + bias[e];
             uint32_t pos = top_k;
             for (uint32_t r = 0; r < top_k; r++) {
                 if (c > choice[r] || (c == choice[r] && e < id[r])) {
@@ -748,64 +771,98 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
         }
     }
 
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int64_t job = 0; job < (int64_t)n * K; job++) {
-        const uint32_t i = (uint32_t)(job / K), r = (uint32_t)(job % K);
-        const uint32_t t = token_list ? token_list[i] : i;
-        const uint16_t *x = hidden_in + (uint64_t)t * H;
-        const k3o_expert *ex = &experts[ids[(uint64_t)i * K + r]];
-        uint16_t *g = (uint16_t *)malloc(2u * F), *u = (uint16_t *)malloc(2u * F);
-        uint16_t *a = (uint16_t *)malloc(2u * F);
-        const int ord = gemv_order;
-        uint8_t *xq = NULL, *xs = NULL, *aq = NULL, *as = NULL;
-        uint8_t *xq2 = NULL, *xs2 = NULL, *aq2 = NULL, *as2 = NULL;
-        if (ord == 3 || ord == 4) {
-            xq = (uint8_t *)malloc(H); xs = (uint8_t *)malloc(H / 32u);
-            aq = (uint8_t *)malloc(F); as = (uint8_t *)malloc(F / 32u);
-            xq2 = (uint8_t *)malloc(H); xs2 = (uint8_t *)malloc(H / 32u);
-            aq2 = (uint8_t *)malloc(F); as2 = (uint8_t *)malloc(F / 32u);
-            if (ord == 3) k3o_mx8_quantize(xq, xs, x, H);
-            else k3o_mx8_split(xq, xs, xq2, xs2, x, H);
+    {
+        /* (route, 64-row block) work items, so every core has work even at
+         * one token; each output row is computed exactly as before. */
+        const uint64_t J = (uint64_t)n * K, RB = 64u;
+        const uint64_t nb_f = (F + RB - 1u) / RB, nb_h = (H + RB - 1u) / RB;
+        const int ord = gemv_order, mx = (ord == 3 || ord == 4);
+        uint16_t *g = (uint16_t *)malloc(2u * J * F), *u = (uint16_t *)malloc(2u * J * F);
+        uint16_t *a = (uint16_t *)malloc(2u * J * F);
+        uint8_t *xq = NULL, *xs = NULL, *xq2 = NULL, *xs2 = NULL;
+        uint8_t *aq = NULL, *as = NULL, *aq2 = NULL, *as2 = NULL;
+        if (mx) {
+            xq = (uint8_t *)malloc((uint64_t)n * H); xs = (uint8_t *)malloc((uint64_t)n * H / 32u);
+            xq2 = (uint8_t *)malloc((uint64_t)n * H); xs2 = (uint8_t *)malloc((uint64_t)n * H / 32u);
+            aq = (uint8_t *)malloc(J * F); as = (uint8_t *)malloc(J * F / 32u);
+            aq2 = (uint8_t *)malloc(J * F); as2 = (uint8_t *)malloc(J * F / 32u);
         }
-        for (uint32_t row = 0; row < F; row++) {
-            const uint64_t po = (uint64_t)row * (H / 2u), so = (uint64_t)row * (H / 32u);
-            float vg, vu;
-            if (ord == 0) {
-                vg = mx_row_w64(ex->w1_packed + po, ex->w1_scales + so, x, H);
-                vu = mx_row_w64(ex->w3_packed + po, ex->w3_scales + so, x, H);
-            } else if (ord == 1) {
-                vg = mx_row_ref128(ex->w1_packed + po, ex->w1_scales + so, x, H);
-                vu = mx_row_ref128(ex->w3_packed + po, ex->w3_scales + so, x, H);
-            } else if (ord == 3) {
-                vg = (float)mx_row_mx8(ex->w1_packed + po, ex->w1_scales + so, xq, xs, H);
-                vu = (float)mx_row_mx8(ex->w3_packed + po, ex->w3_scales + so, xq, xs, H);
-            } else if (ord == 4) {
-                vg = (float)mx_row_split(ex->w1_packed + po, ex->w1_scales + so, xq, xs, xq2, xs2, H);
-                vu = (float)mx_row_split(ex->w3_packed + po, ex->w3_scales + so, xq, xs, xq2, xs2, H);
-            } else {
-                vg = (float)mx_row_f64(ex->w1_packed + po, ex->w1_scales + so, x, H);
-                vu = (float)mx_row_f64(ex->w3_packed + po, ex->w3_scales + so, x, H);
+        if (!g || !u || !a || (mx && (!xq || !xs || !xq2 || !xs2 || !aq || !as || !aq2 || !as2))) {
+            status = -2;
+        } else {
+            if (mx) {
+#pragma omp parallel for schedule(static)
+                for (int64_t i = 0; i < (int64_t)n; i++) {
+                    const uint32_t t = token_list ? token_list[i] : (uint32_t)i;
+                    const uint16_t *x = hidden_in + (uint64_t)t * H;
+                    const uint64_t o = (uint64_t)i * H;
+                    if (ord == 3) k3o_mx8_quantize(xq + o, xs + o / 32u, x, H);
+                    else k3o_mx8_split(xq + o, xs + o / 32u, xq2 + o, xs2 + o / 32u, x, H);
+                }
             }
-            g[row] = k3o_f32_to_bf16(vg);
-            u[row] = k3o_f32_to_bf16(vu);
+#pragma omp parallel for schedule(dynamic, 1)
+            for (int64_t item = 0; item < (int64_t)(J * nb_f); item++) {
+                const uint64_t job = (uint64_t)item / nb_f, r0 = ((uint64_t)item % nb_f) * RB;
+                const uint32_t i = (uint32_t)(job / K);
+                const uint32_t t = token_list ? token_list[i] : i;
+                const uint16_t *x = hidden_in + (uint64_t)t * H;
+                const k3o_expert *ex = &experts[ids[job]];
+                const uint64_t xo = (uint64_t)i * H;
+                for (uint64_t row = r0; row < r0 + RB && row < F; row++) {
+                    const uint64_t po = row * (H / 2u), so = row * (H / 32u);
+                    float vg, vu;
+                    if (ord == 0) {
+                        vg = mx_row_w64(ex->w1_packed + po, ex->w1_scales + so, x, H);
+                        vu = mx_row_w64(ex->w3_packed + po, ex->w3_scales + so, x, H);
+                    } else if (ord == 1) {
+                        vg = mx_row_ref128(ex->w1_packed + po, ex->w1_scales + so, x, H);
+                        vu = mx_row_ref128(ex->w3_packed + po, ex->w3_scales + so, x, H);
+                    } else if (ord == 3) {
+                        vg = (float)mx_row_mx8(ex->w1_packed + po, ex->w1_scales + so, xq + xo, xs + xo / 32u, H);
+                        vu = (float)mx_row_mx8(ex->w3_packed + po, ex->w3_scales + so, xq + xo, xs + xo / 32u, H);
+                    } else if (ord == 4) {
+                        vg = (float)mx_row_split(ex->w1_packed + po, ex->w1_scales + so, xq + xo, xs + xo / 32u,
+                                                 xq2 + xo, xs2 + xo / 32u, H);
+                        vu = (float)mx_row_split(ex->w3_packed + po, ex->w3_scales + so, xq + xo, xs + xo / 32u,
+                                                 xq2 + xo, xs2 + xo / 32u, H);
+                    } else {
+                        vg = (float)mx_row_f64(ex->w1_packed + po, ex->w1_scales + so, x, H);
+                        vu = (float)mx_row_f64(ex->w3_packed + po, ex->w3_scales + so, x, H);
+                    }
+                    g[job * F + row] = k3o_f32_to_bf16(vg);
+                    u[job * F + row] = k3o_f32_to_bf16(vu);
+                }
+            }
+#pragma omp parallel for schedule(static)
+            for (int64_t job = 0; job < (int64_t)J; job++) {
+                const uint64_t o = (uint64_t)job * F;
+                if (sh->activation == 1u) k3o_swiglu(a + o, g + o, u + o, F, 0);
+                else k3o_situ(a + o, g + o, u + o, F, sh->beta, sh->linear_beta, 0);
+                if (ord == 3) k3o_mx8_quantize(aq + o, as + o / 32u, a + o, F);
+                if (ord == 4) k3o_mx8_split(aq + o, as + o / 32u, aq2 + o, as2 + o / 32u, a + o, F);
+            }
+#pragma omp parallel for schedule(dynamic, 1)
+            for (int64_t item = 0; item < (int64_t)(J * nb_h); item++) {
+                const uint64_t job = (uint64_t)item / nb_h, r0 = ((uint64_t)item % nb_h) * RB;
+                const k3o_expert *ex = &experts[ids[job]];
+                const uint64_t ao = job * F;
+                uint16_t *y = ys + job * H;
+                for (uint64_t row = r0; row < r0 + RB && row < H; row++) {
+                    const uint64_t po = row * (F / 2u), so = row * (F / 32u);
+                    float v;
+                    if (ord == 0) v = mx_row_w64(ex->w2_packed + po, ex->w2_scales + so, a + ao, F);
+                    else if (ord == 1) v = mx_row_ref128(ex->w2_packed + po, ex->w2_scales + so, a + ao, F);
+                    else if (ord == 3) v = (float)mx_row_mx8(ex->w2_packed + po, ex->w2_scales + so, aq + ao, as + ao / 32u, F);
+                    else if (ord == 4) v = (float)mx_row_split(ex->w2_packed + po, ex->w2_scales + so, aq + ao, as + ao / 32u,
+                                                               aq2 + ao, as2 + ao / 32u, F);
+                    else v = (float)mx_row_f64(ex->w2_packed + po, ex->w2_scales + so, a + ao, F);
+                    y[row] = k3o_f32_to_bf16(v);
+                }
+            }
         }
-        if (sh->activation == 1u) k3o_swiglu(a, g, u, F, 0);
-        else k3o_situ(a, g, u, F, sh->beta, sh->linear_beta, 0);
-        if (ord == 3) k3o_mx8_quantize(aq, as, a, F);
-        if (ord == 4) k3o_mx8_split(aq, as, aq2, as2, a, F);
-        uint16_t *y = ys + ((uint64_t)i * K + r) * H;
-        for (uint32_t row = 0; row < H; row++) {
-            const uint64_t po = (uint64_t)row * (F / 2u), so = (uint64_t)row * (F / 32u);
-            float v;
-            if (ord == 0) v = mx_row_w64(ex->w2_packed + po, ex->w2_scales + so, a, F);
-            else if (ord == 1) v = mx_row_ref128(ex->w2_packed + po, ex->w2_scales + so, a, F);
-            else if (ord == 3) v = (float)mx_row_mx8(ex->w2_packed + po, ex->w2_scales + so, aq, as, F);
-            else if (ord == 4) v = (float)mx_row_split(ex->w2_packed + po, ex->w2_scales + so, aq, as, aq2, as2, F);
-            else v = (float)mx_row_f64(ex->w2_packed + po, ex->w2_scales + so, a, F);
-            y[row] = k3o_f32_to_bf16(v);
-        }
-        free(g); free(u); free(a); free(xq); free(xs); free(aq); free(as);
-        free(xq2); free(xs2); free(aq2); free(as2);
+        free(g); free(u); free(a); free(xq); free(xs); free(xq2); free(xs2);
+        free(aq); free(as); free(aq2); free(as2);
+        if (status) goto done;
     }
 
     for (uint32_t i = 0; i < n; i++) {

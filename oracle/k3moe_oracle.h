@@ -53,6 +53,7 @@ float    k3o_e8m0(uint8_t exponent);
 float    k3o_expf(float x);
 float    k3o_tanhf(float x);
 float    k3o_sigmoid(float x, int use_libm);
+float    k3o_router_sigmoid(float x);
 
 /* ---- activations (k3_rocm_ops.cu:66-83 SiTU; SwiGLU = limit form) ------ */
 void k3o_situ(uint16_t *out, const uint16_t *gate, const uint16_t *up,

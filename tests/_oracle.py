@@ -54,6 +54,7 @@ def lib():
             "k3o_expf": (_f, [_f]),
             "k3o_tanhf": (_f, [_f]),
             "k3o_sigmoid": (_f, [_f, _i]),
+            "k3o_router_sigmoid": (_f, [_f]),
             "k3o_situ": (None, [_p, _p, _p, _u64, _f, _f, _i]),
             "k3o_swiglu": (None, [_p, _p, _p, _u64, _i]),
             "k3o_router_logits": (None, [_p, _p, _p, _u32, _u32, _u32, _i]),
@@ -102,6 +103,61 @@ def router_topk(logits, bias, k, scale, use_libm=False):
     assert lib().k3o_router_topk(_ptr(ids), _ptr(w), _ptr(np.ascontiguousarray(logits)),
                                  _ptr(bias), T, E, k, scale, int(use_libm)) == 0
     return ids, w
+
+
+def router_choices(logits, bias):
+    """The router's choices as the oracle models the device: router_sigmoid
+    (correctly rounded restatement of the hardware sequence) + bias, fp32."""
+    f = lib().k3o_router_sigmoid
+    s = np.array([f(float(v)) for v in np.ravel(logits)], np.float32).reshape(np.shape(logits))
+    return (s + np.asarray(bias, np.float32)).astype(np.float32)
+
+
+def route_weights(ids, logits, scale):
+    """weight_r = s_r / (1e-20 + sum of the selected s in rank order) * scale
+    with s = k3o_sigmoid(logit, 0), fp32 left to right, for given ids (the
+    top-k's weight formula, k3_rocm_ops.cu:1440-1448)."""
+    f = lib().k3o_sigmoid
+    out = np.zeros(ids.shape, np.float32)
+    for t in range(ids.shape[0]):
+        live = [int(e) for e in ids[t] if e < logits.shape[1]]
+        sc = [np.float32(f(float(logits[t, e]), 0)) for e in live]
+        den = np.float32(1e-20)
+        for v in sc:
+            den = np.float32(den + v)
+        for r, v in enumerate(sc):
+            out[t, r] = np.float32(np.float32(v / den) * np.float32(scale))
+    return out
+
+
+def check_routes(got_ids, got_w, logits, bias, k, scale):
+    """Device routes against the oracle router on the same logits.
+
+    The device orders experts by the hardware sigmoid the reference kernel
+    uses (bit-identical to the reference's ids, tested against it on the
+    GPU); the oracle's restatement of that sigmoid rounds exp2 and the
+    reciprocal correctly, so it can sit up to a few ulp from the device. ids
+    must therefore equal the oracle's except at near-ties: every token whose
+    ids differ must hold a top-k of the oracle's choices when each choice may
+    be off by 4 ulp of the sigmoid plus one rounding of the bias add.
+    Weights are bit-exact to the oracle's formula on the device's own ids.
+    Returns the indices of the tokens whose ids differ."""
+    want_ids, want_w = router_topk(logits, bias, k, scale)
+    bad = np.nonzero((np.asarray(got_ids) != want_ids).any(axis=1))[0]
+    for t in bad:
+        c = router_choices(logits[t], bias).astype(np.float64)
+        tol = 4 * 2.0 ** -24 + 2.0 ** -23 * np.abs(c)
+        sel = np.asarray(got_ids[t], np.int64)
+        live = sel[sel < c.size]
+        for a, b in zip(live[:-1], live[1:]):
+            assert c[a] >= c[b] - (tol[a] + tol[b]), f"token {t}: ranks out of order"
+        rest = np.setdiff1d(np.arange(c.size), live)
+        if rest.size and live.size:
+            assert (c[live] + tol[live]).min() >= (c[rest] - tol[rest]).max(), \
+                f"token {t}: routes are not a near-tie of the oracle's top-k"
+        want_w[t] = route_weights(np.asarray(got_ids[t:t + 1]), logits[t:t + 1], scale)[0]
+    np.testing.assert_array_equal(np.asarray(got_w), want_w)
+    return bad
 
 
 def route_plan(ids, experts):

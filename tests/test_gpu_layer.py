@@ -13,7 +13,7 @@ import torch
 import _oracle as O
 from moonshine_amd import layer as L
 from moonshine_amd._lib import lib
-from moonshine_amd.synth import CONFIGS, K3_NATIVE, Config, make_inputs
+from moonshine_amd.synth import CONFIGS, K3_NATIVE, Config, bf16_bits_to_f32, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -66,14 +66,18 @@ def run_profiled(cfg, inputs, moe, cuda):
 
 
 def host_experts(store, ids):
-    return {int(e): store.host_expert(int(e)) for e in np.unique(ids)}
+    """The selected experts' six tensors, copied from the device store
+    (test_synth_store_host_matches_device pins them to the host generator)."""
+    return {int(e): [t.cpu().numpy() for t in store.device_expert(int(e))]
+            for e in np.unique(ids) if e < store.experts}
 
 
 def check_tokens(cfg, inputs, store, got_out, got_ids, got_w, tokens):
+    """Output bits of the listed tokens against the oracle layer run on the
+    device's routes (the routes themselves are checked by the caller)."""
     tokens = np.asarray(tokens, dtype=np.uint32)
-    want = O.layer(cfg, inputs, host_experts(store, got_ids[tokens]), tokens=tokens)
-    np.testing.assert_array_equal(got_ids[tokens], want["ids"])
-    np.testing.assert_array_equal(got_w[tokens], want["weights"])
+    want = O.layer(cfg, inputs, host_experts(store, got_ids[tokens]), tokens=tokens,
+                   ids=np.ascontiguousarray(got_ids), weights=np.ascontiguousarray(got_w))
     np.testing.assert_array_equal(got_out[tokens], want["output"])
 
 
@@ -196,7 +200,7 @@ def test_missing_routes(cuda, T):
     np.testing.assert_array_equal(out, want["output"])
 
 
-@pytest.mark.parametrize("cfg_index,check", [(0, None), (2, 12), (3, 6)])
+@pytest.mark.parametrize("cfg_index,check", [(0, None), (2, 16), (3, 32)])
 def test_batched_layer_bitexact(cuda, cfg_index, check):
     cfg = CONFIGS[cfg_index]
     T = cfg.tokens if cfg_index else 40
@@ -205,9 +209,8 @@ def test_batched_layer_bitexact(cuda, cfg_index, check):
     out, ids, w = run(cfg, inputs, moe, cuda)
     # routing of every token is checked against the oracle router
     want_logits = O.router_logits(inputs.router_weight, inputs.hidden)
-    want_ids, want_w = O.router_topk(want_logits, inputs.router_bias, cfg.top_k, cfg.scale)
-    np.testing.assert_array_equal(ids, want_ids)
-    np.testing.assert_array_equal(w, want_w)
+    bad = O.check_routes(ids, w, want_logits, inputs.router_bias, cfg.top_k, cfg.scale)
+    assert bad.size <= max(1, T // 1000)
     rng = np.random.default_rng(5)
     tokens = np.arange(T) if check is None else np.sort(rng.choice(T, check, replace=False))
     check_tokens(cfg, inputs, moe.store, out, ids, w, tokens)
@@ -218,6 +221,86 @@ def test_batched_layer_bitexact(cuda, cfg_index, check):
     o1, i1, w1 = run(cfg, one, moe, cuda)
     np.testing.assert_array_equal(i1[0], ids[t])
     np.testing.assert_array_equal(o1[0], out[t])
+
+
+def plan_of(ids, E, cuda):
+    """k3_moe_route_plan (the plan kernels the layer runs) on given routes."""
+    T, k = ids.shape
+    d_ids = torch.from_numpy(np.ascontiguousarray(ids).view(np.int32)).to(cuda)
+    counts = torch.zeros(E, dtype=torch.int32, device=cuda)
+    offsets = torch.zeros(E + 1, dtype=torch.int32, device=cuda)
+    unique = torch.zeros(E, dtype=torch.int32, device=cuda)
+    summary = torch.zeros(4, dtype=torch.int32, device=cuda)
+    tok = torch.zeros(T * k, dtype=torch.int32, device=cuda)
+    route = torch.zeros(T * k, dtype=torch.int32, device=cuda)
+    nscratch = lib().k3_moe_plan_scratch_bytes(T, E)
+    scratch = torch.zeros(nscratch, dtype=torch.uint8, device=cuda)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    assert lib().k3_moe_route_plan(P(counts), P(offsets), P(unique), P(summary), P(tok), P(route),
+                                   P(d_ids), T, k, E, P(scratch), nscratch,
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    h = lambda t: t.cpu().numpy().view(np.uint32)
+    n = int(h(summary)[0])
+    return h(counts), h(offsets), h(unique)[:n], h(tok), h(route)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("precision", [0, 1], ids=["exact", "mfma"])
+def test_cfg4_full_routes_and_sample_vs_oracle(cuda, precision):
+    """BASELINE config 4 at full size (8192 tokens, Zipf bias): every
+    token's ids equal to the C oracle router's or a near-tie of it within
+    the ulps of its sigmoid restatement (O.check_routes), and every weight
+    bit-equal to the oracle's formula on those ids; the plan of
+    the layer's routes equal to the oracle's stable-sort plan; output bits
+    of 24 tokens (up to 9 of them routed to the three heaviest experts, and
+    every near-tie token) equal to
+    the oracle on the exact path, and inside the MFMA tolerance (rel-L2
+    <= 2e-3, 4 bf16 ulp of max(|v|, RMS)) on the MFMA path."""
+    cfg = CONFIGS[4]
+    T = cfg.tokens
+    inputs = make_inputs(cfg)
+    moe = get_layer(cfg, inputs, cuda)
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    ids_d = torch.zeros((T, cfg.top_k), dtype=torch.int32, device=cuda)
+    w_d = torch.zeros((T, cfg.top_k), dtype=torch.float32, device=cuda)
+    out_d = moe.forward(x, r, ids=ids_d, weights=w_d, precision=precision)
+    torch.cuda.synchronize()
+    out, ids, w = L.bf16_bits(out_d), ids_d.cpu().numpy().view(np.uint32), w_d.cpu().numpy()
+    logits = O.router_logits(inputs.router_weight, inputs.hidden)
+    bad = O.check_routes(ids, w, logits, inputs.router_bias, cfg.top_k, cfg.scale)
+    print(f"\ncfg4: {bad.size}/{T} tokens' ids differ from the oracle router, all near-ties "
+          f"within the ulps of its sigmoid restatement")
+    assert bad.size <= 4
+    c, o, u, t_i, r_i = O.route_plan(ids, cfg.experts)
+    gc, go, gu, gt, gr = plan_of(ids, cfg.experts, cuda)
+    for a, b in ((gc, c), (go, o), (gu, u), (gt, t_i), (gr, r_i)):
+        np.testing.assert_array_equal(a, b)
+    heavy = np.argsort(-c, kind="stable")[:3]
+    print(f"\ncfg4: U = {u.size}, heaviest experts {heavy.tolist()} with {c[heavy].tolist()} rows")
+    rng = np.random.default_rng(44)
+    picks = set()
+    for e in heavy:
+        rows = t_i[o[e]:o[e + 1]]
+        picks.update(rng.choice(rows, min(3, rows.size), replace=False).tolist())
+    picks.update(int(t) for t in bad)
+    picks.update(rng.choice(T, 24 - len(picks), replace=False).tolist())
+    tokens = np.array(sorted(picks), dtype=np.uint32)
+    assert tokens.size >= 16
+    if precision == 0:
+        check_tokens(cfg, inputs, moe.store, out, ids, w, tokens)
+    else:
+        want = O.layer(cfg, inputs, host_experts(moe.store, ids[tokens]), tokens=tokens, ids=ids,
+                       weights=w)
+        g = bf16_bits_to_f32(out[tokens]).astype(np.float64)
+        f = bf16_bits_to_f32(want["output"]).astype(np.float64)
+        rel = np.linalg.norm(g - f) / np.linalg.norm(f)
+        rms = np.sqrt(np.mean(f * f))
+        lim = 4 * 2.0 ** (np.floor(np.log2(np.maximum(np.abs(f), rms))) - 7)
+        print(f"cfg4 MFMA vs oracle on {tokens.size} tokens: rel-L2 {rel:.3g}")
+        assert rel <= 2e-3
+        assert (np.abs(g - f) <= lim).all()
 
 
 def test_expert_stage_on_given_routes(cuda):

@@ -116,3 +116,65 @@ def test_certified_router_adversarial(cuda):
     assert (ids[9:] >= 0).all()
     big_bias = rng.normal(0, 10.0, E).astype(np.float32)
     check(w, big_bias, x, k, 1.0, cuda)
+
+
+def test_router_sigmoid_exhaustive_bound(cuda):
+    """The router's choice sigmoid (the reference's hardware exp2/reciprocal
+    sequence, k3_moe_router_choices_f32 with no bias) on EVERY fp32 logit in
+    [-100, 100]: within 3e-7 of the real sigmoid, the bound the certified
+    router's choice error (k3_router.hip) assumes. Also the share of inputs
+    where the CPU restatement k3o_router_sigmoid (correctly rounded exp2 and
+    reciprocal) equals the device bits, on a random sample."""
+    import _oracle as O
+    worst = 0.0
+    top = np.float32(100.0).view(np.int32)
+    step = 1 << 27
+    for sign in (0, 1 << 31):
+        for lo in range(0, int(top) + 1, step):
+            hi = min(lo + step, int(top) + 1)
+            bits = torch.arange(lo, hi, dtype=torch.int64, device=cuda)
+            bits = (bits | sign).to(torch.int64)
+            bits = torch.where(bits >= 1 << 31, bits - (1 << 32), bits).to(torch.int32)
+            x = bits.view(torch.float32)
+            out = torch.empty_like(x)
+            assert lib().k3_moe_router_choices_f32(ctypes.c_void_p(out.data_ptr()),
+                                                   ctypes.c_void_p(x.data_ptr()), None, 1,
+                                                   x.numel(), None)
+            ref = torch.sigmoid(x.double())
+            worst = max(worst, float((out.double() - ref).abs().max()))
+            del bits, x, out, ref
+    print(f"\nrouter sigmoid: worst |s - sigmoid| over all fp32 in [-100, 100] = {worst:.3g}")
+    assert worst <= 3e-7
+    rng = np.random.default_rng(3)
+    xs = np.concatenate([rng.normal(0, 3, 100000), rng.uniform(-40, 40, 100000)]).astype(np.float32)
+    out = torch.empty(xs.size, dtype=torch.float32, device=cuda)
+    assert lib().k3_moe_router_choices_f32(ctypes.c_void_p(out.data_ptr()),
+                                           ctypes.c_void_p(dev(xs, cuda).data_ptr()), None, 1,
+                                           xs.size, None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    emu = np.array([O.lib().k3o_router_sigmoid(float(v)) for v in xs], np.float32)
+    same = float((got.view(np.uint32) == emu.view(np.uint32)).mean())
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - emu.view(np.int32).astype(np.int64))
+    i = int(np.argmax(ulps))
+    print(f"router sigmoid: CPU restatement equals the device on {same:.4%} of "
+          f"{xs.size} inputs, max {ulps.max()} ulp apart (at x = {xs[i]!r})")
+    assert same >= 0.8
+    assert np.abs(got.astype(np.float64) - emu).max() <= 4 * 2.0 ** -24
+
+
+def test_router_choices_with_bias(cuda):
+    rng = np.random.default_rng(5)
+    T, E = 3, 896
+    lg = rng.normal(0, 2, (T, E)).astype(np.float32)
+    b = rng.normal(0, 0.1, E).astype(np.float32)
+    out = torch.empty((T, E), dtype=torch.float32, device=cuda)
+    s = torch.empty((T, E), dtype=torch.float32, device=cuda)
+    dl = dev(lg, cuda)
+    assert lib().k3_moe_router_choices_f32(ctypes.c_void_p(out.data_ptr()),
+                                           ctypes.c_void_p(dl.data_ptr()),
+                                           ctypes.c_void_p(dev(b, cuda).data_ptr()), T, E, None)
+    assert lib().k3_moe_router_choices_f32(ctypes.c_void_p(s.data_ptr()),
+                                           ctypes.c_void_p(dl.data_ptr()), None, T, E, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), (s.cpu().numpy() + b).astype(np.float32))

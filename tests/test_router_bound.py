@@ -1,15 +1,20 @@
 """CPU checks of what the certified MFMA router (k3_router.hip) relies on:
 
-1. the deterministic sigmoid (the oracle's k3o_sigmoid(x, 0) evaluates the
-   device's sequence) is within 3e-7 of the real sigmoid everywhere, which
-   the 2e-6 absolute slack of the choice bound covers twice over;
+1. the choice sigmoid is within 3e-7 of the real sigmoid everywhere. The
+   device evaluates the reference's hardware exp2/reciprocal sequence
+   (router_sigmoid; pinned on the part by an exhaustive sweep in
+   test_gpu_router.py); its CPU restatement k3o_router_sigmoid is checked
+   here. The 2e-6 absolute slack of the choice bound covers the error of
+   both the approximate and the exact choice twice over;
 2. the candidate rule keeps every expert of the exact top-k: with exact
    logits l, approximate logits a anywhere within |a - l| <= err, choices
    c = sigmoid + bias, ce = s'(max(0, |a| - err)) err + 2e-6 + 2^-21 |c|,
    T_k the k-th largest approximate choice and E_k the largest ce at or
    above it, the exact top-k (ties towards the lower id) satisfies
    c~ + ce >= T_k - E_k. Brute force over random and adversarial cases
-   (errors pushed to the bound against the true order, exact ties).
+   (errors pushed to the bound against the true order, exact ties), with
+   the slope and ce formed in fp32 in the kernel's order from the
+   deterministic sigmoid the kernel uses for the slope.
 """
 import numpy as np
 
@@ -24,9 +29,19 @@ def sig64(z):
 
 def test_deterministic_sigmoid_error():
     z = np.concatenate([np.linspace(-90, 90, 400001), np.linspace(-4, 4, 100001)]).astype(np.float32)
-    got = np.array([L.k3o_sigmoid(float(v), 0) for v in z[::5]], np.float64)
     want = sig64(z[::5].astype(np.float64))
-    assert np.abs(got - want).max() <= 3e-7
+    for fn in (lambda v: L.k3o_sigmoid(v, 0), L.k3o_router_sigmoid):
+        got = np.array([fn(float(v)) for v in z[::5]], np.float64)
+        assert np.abs(got - want).max() <= 3e-7
+
+
+def f32(v):
+    return np.float32(v)
+
+
+def fmaf(a, b, c):
+    """fp32 fused multiply-add: the fp32 product is exact in fp64."""
+    return f32(np.float64(a) * np.float64(b) + np.float64(c))
 
 
 def det_sigmoid_f32(z, rng):
@@ -38,10 +53,14 @@ def det_sigmoid_f32(z, rng):
 def candidates(a, err, bias, k, rng):
     s = det_sigmoid_f32(a, rng)
     ch = (s + bias).astype(np.float32)
-    m = np.maximum(0.0, np.abs(a) - err).astype(np.float32)
-    sm = sig64(m.astype(np.float64))
-    slope = (sm * (1 - sm) * (1 + 2.0 ** -10)).astype(np.float32)
-    ce = (slope * err + 2e-6 + 4.76837158203125e-7 * np.abs(ch)).astype(np.float32)
+    # the kernel's fp32 sequence: m = max(0, |a| - err); sm = det_sigmoid(m);
+    # slope = (sm * (1 - sm)) * (1 + 2^-10); ce = fma(slope, err, fma(2^-21, |c|, 2e-6))
+    m = np.maximum(np.float32(0), (np.abs(a) - err).astype(np.float32)).astype(np.float32)
+    sm = np.array([L.k3o_sigmoid(float(v), 0) for v in m], np.float32)
+    slope = ((sm * (np.float32(1) - sm)).astype(np.float32) *
+             np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
+    ce = np.array([fmaf(slope[i], err[i], fmaf(4.76837158203125e-7, abs(ch[i]), 2e-6))
+                   for i in range(len(ch))], np.float32)
     order = np.lexsort((np.arange(len(ch)), -ch.astype(np.float64)))
     tk = ch[order[k - 1]]
     ek = ce[ch >= tk].max()
@@ -69,7 +88,11 @@ def test_candidate_rule_keeps_exact_topk():
         bias = (rng.normal(0, float(rng.choice([0.0, 0.01, 0.5, 5.0])), E)).astype(np.float32)
         if trial % 11 == 0:
             bias[:] = bias[0]
+        if trial % 5 == 0:  # logits out in the sigmoid's tail, small and large errors
+            l = (rng.choice([-1.0, 1.0], E) * rng.uniform(8.0, 17.0, E)).astype(np.float32)
         err = (np.abs(rng.normal(0, 0.01, E)) * float(rng.choice([0.01, 1.0, 30.0]))).astype(np.float32)
+        if trial % 13 == 0:
+            err = rng.uniform(10.0, 100.0, E).astype(np.float32)
         # approximate logits: random within the bound, or pushed to the bound
         # against the exact order (top experts down, the rest up)
         if trial % 2:
