@@ -167,6 +167,28 @@ bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
                          size_t workspace_bytes, void *stream);
 
 /*
+ * k3_moe_forward_bf16 without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The workspace is a static device array of
+ * K3_MOE_STATIC_WORKSPACE_BYTES per GPU, held until the process ends;
+ * its address is looked up once per device on the first call there. A
+ * shape / token count whose k3_moe_workspace_bytes() exceeds it is
+ * rejected (false, with a message on stderr): at the K3 config (H 7168,
+ * E 896, k 16, F 2048) up to 64 tokens fit. The call allocates nothing.
+ * Every call on one GPU shares that GPU's array: calls that may overlap
+ * on one GPU (two streams, two host threads) race and must be serialised
+ * by the caller. Arguments otherwise as k3_moe_forward_bf16.
+ */
+#define K3_MOE_STATIC_WORKSPACE_BYTES (32u << 20)
+bool k3_moe_forward_static_bf16(void *output, const void *hidden, const void *residual,
+                                const void *router_weight, const void *router_bias,
+                                const k3_moe_expert *experts,
+                                const k3_moe_shape *shape, uint32_t token_count,
+                                uint32_t precision, void *expert_ids,
+                                void *expert_weights, void *stream);
+
+/*
  * Stage boundaries of k3_moe_forward_profiled_bf16. stage_events[i] (a
  * hipEvent_t, or NULL) is recorded on the stream just before stage i is
  * launched; stage_events[K3_MOE_STAGE_END] after the last one. Stages a

@@ -28,7 +28,9 @@
 #include "../../include/k3_rocm_ops.h"
 
 #include <hip/hip_runtime.h>
+#include <mutex>
 #include <stdint.h>
+#include <stdio.h>
 #include <string.h>
 
 using namespace k3;
@@ -711,6 +713,68 @@ extern "C" bool k3_moe_forward_bf16(void *output, const void *hidden, const void
                                         experts, shape, token_count, precision, expert_ids,
                                         expert_weights, workspace, workspace_bytes, nullptr,
                                         stream);
+}
+
+/* ======================================================================== */
+/* Workspace-free entry point                                                */
+/* ======================================================================== */
+
+/*
+ * The workspace of k3_moe_forward_static_bf16: one array per GPU, held
+ * until the process ends. Host code never uses the array's name as an
+ * address (on the host it is only a stand-in for the symbol): the device
+ * address of the current GPU's copy comes from hipGetSymbolAddress, once
+ * per device, and only that pointer is passed to kernels.
+ */
+static __device__ __align__(256) uint8_t scratch[K3_MOE_STATIC_WORKSPACE_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];
+
+/* Device address of the current GPU's scratch array, or nullptr. */
+void *static_workspace() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            fprintf(stderr, "k3_moe_forward_static_bf16: hipGetSymbolAddress failed on device %d\n",
+                    dev);
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" bool k3_moe_forward_static_bf16(void *output, const void *hidden, const void *residual,
+                                           const void *router_weight, const void *router_bias,
+                                           const k3_moe_expert *experts,
+                                           const k3_moe_shape *shape, uint32_t token_count,
+                                           uint32_t precision, void *expert_ids,
+                                           void *expert_weights, void *stream) {
+    const size_t need = k3_moe_workspace_bytes(shape, token_count);
+    if (need == 0u) return false;
+    if (need > (size_t)K3_MOE_STATIC_WORKSPACE_BYTES) {
+        fprintf(stderr,
+                "k3_moe_forward_static_bf16: %u tokens need %zu bytes of workspace, above the "
+                "static maximum of %u bytes; use k3_moe_forward_bf16 with a caller workspace\n",
+                token_count, need, (unsigned)K3_MOE_STATIC_WORKSPACE_BYTES);
+        return false;
+    }
+    void *ws = static_workspace();
+    if (!ws) return false;
+    /* The layer keeps no state in its workspace between calls (every
+     * buffer is written before it is read), so nothing is cleared here. */
+    return k3_moe_forward_profiled_bf16(output, hidden, residual, router_weight, router_bias,
+                                        experts, shape, token_count, precision, expert_ids,
+                                        expert_weights, ws, need, nullptr, stream);
 }
 
 extern "C" bool k3_moe_synth_fill(void *base, uint64_t bytes, uint64_t seed, uint64_t stream_id,
