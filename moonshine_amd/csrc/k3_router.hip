@@ -49,6 +49,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 namespace k3 {
 namespace {
@@ -485,9 +486,26 @@ uint32_t router_slices(uint32_t T, uint32_t E, uint32_t H) {
     return ks == 0u ? 1u : (S < ks ? S : ks);
 }
 
+/* The certified bound assumes the MFMA unit's per-instruction error measured
+ * on gfx950 (4 u per term allowed, 8 u sum|p| worst seen): on any other
+ * part the exact router runs. The answer is cached per device (benign race:
+ * every writer stores the same value). */
+static bool device_is_gfx950() {
+    static signed char cache[64];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (cache[dev] == 0) {
+        hipDeviceProp_t prop;
+        const bool ok = hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+                        strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+        cache[dev] = ok ? 1 : -1;
+    }
+    return cache[dev] > 0;
+}
+
 bool router_certified_supported(uint32_t tokens, uint32_t experts, uint32_t hidden,
                                 uint32_t top_k, const void *router_weight, const void *x) {
-    return tokens > 0u && experts >= top_k && experts <= 64u * (uint32_t)kTopkSlots &&
+    return device_is_gfx950() && tokens > 0u && experts >= top_k && experts <= 64u * (uint32_t)kTopkSlots &&
            top_k >= 1u && top_k <= 32u && hidden > 0u && hidden % kRK == 0u &&
            hidden <= 8u * 64u * (uint32_t)kTopkSlots &&
            (((uintptr_t)router_weight | (uintptr_t)x) % 16u) == 0u;
