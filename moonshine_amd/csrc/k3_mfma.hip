@@ -421,6 +421,37 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         bv[j] = ds_read16<(C::KS == 2 ? 2048 : 1024) * j>(b_base);
         sbw[j] = ds_read4<256 * j>(sb_base);
     });
+#ifndef K3_MFMA_NOPIPE
+    if constexpr (C::SEQ) {
+        /* Software pipeline over the A fragments: the reads of fragment
+         * q + 1 are issued before the MFMAs of fragment q, so the LDS
+         * reads run under the matrix pipe instead of in a read phase
+         * with no MFMA in flight. Two fragment registers sets; LDS reads
+         * complete in order, so lgkmcnt(3) = all but fragment q + 1. */
+        read_a(std::integral_constant<int, 0>{});
+        static_for<NA>([&](auto Q) {
+            constexpr int q = decltype(Q)::value;
+            if constexpr (q + 1 < NA) {
+                read_a(std::integral_constant<int, q + 1>{});
+                wait_lgkm<3>();
+            } else {
+                wait_lgkm<0>();
+            }
+            if constexpr (q == 0) {
+                static_for<C::WN>([&](auto J) {
+                    after_wait(bv[decltype(J)::value]);
+                    after_wait(sbw[decltype(J)::value]);
+                });
+            }
+            after_wait(alo[q]);
+            after_wait(ahi[q]);
+            after_wait(saw[q]);
+            mfmas(Q);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        return;
+    }
+#endif
     if constexpr (C::SEQ) {
         /* register-bound tiles: the second half's fragments are read into
          * the registers the first half frees, after its MFMAs are issued */
