@@ -388,3 +388,93 @@ def test_decode_vs_reference_composition(cuda, cfg, T):
                              torch.from_numpy(wr).to(cuda), r)
         sync()
         check_outputs(L.bf16_bits(o)[bad], want[bad], f"{cfg.name} experts on reference routes")
+
+
+# ---- 4. the reference's prefill composition -------------------------------
+
+def reference_prefill(cfg, moe, x, r, cuda):
+    """A token batch through the reference's kernels in the prefill engine's
+    order (k3_engine_prefill.inc:1448-1460 router, the expert-major plan of
+    :1175-1194, per expert launch_prefill_expert :938-997 -- gather, gate and
+    up MXFP4 GEMMs, activation, down GEMM, scatter into the route slots --
+    then :1557-1609 weighted sum and residual add)."""
+    T, E, k, H, F = x.shape[0], cfg.experts, cfg.top_k, cfg.hidden, cfg.ffn
+    R = ref()
+    for name in ("k3_rocm_mxfp4_gemm_bf16", "k3_rocm_gather_rows_bf16",
+                 "k3_rocm_scatter_rows_bf16", "k3_rocm_weighted_sum_bf16_batch"):
+        res, args = SIGNATURES[name]
+        fn = getattr(R.h, name)
+        fn.restype, fn.argtypes = res, args
+    logits = torch.zeros((T, E), dtype=torch.float32, device=cuda)
+    ids = torch.zeros((T, k), dtype=torch.int32, device=cuda)
+    w = torch.zeros((T, k), dtype=torch.float32, device=cuda)
+    R.bf16_gemm_f32(logits, moe.router_weight, x, T, E, H)
+    R.router_topk_f32_batch(ids, w, logits, moe.router_bias, T, E, k, ctypes.c_float(cfg.scale))
+    sync()
+    ids_h = u32(ids)
+    counts, offsets, unique, tok, route = O.route_plan(ids_h, E)
+    tok_d = torch.from_numpy(tok.view(np.int32)).to(cuda)
+    route_d = torch.from_numpy(route.view(np.int32)).to(cuda)
+    nmax = int(counts.max())
+    xg = torch.zeros((nmax, H), dtype=torch.bfloat16, device=cuda)
+    g = torch.zeros((nmax, F), dtype=torch.bfloat16, device=cuda)
+    u = torch.zeros_like(g)
+    a = torch.zeros_like(g)
+    yo = torch.zeros((nmax, H), dtype=torch.bfloat16, device=cuda)
+    slots = torch.zeros((T * k, H), dtype=torch.bfloat16, device=cuda)
+    for e in unique:
+        n, o = int(counts[e]), int(offsets[e])
+        gp, gs, dp, ds, up, us = moe.store.device_expert(int(e))
+        R.gather_rows_bf16(xg, x, tok_d[o:o + n], n, H)
+        R.mxfp4_gemm_bf16(g, gp, gs, xg, n, F, H)
+        R.mxfp4_gemm_bf16(u, up, us, xg, n, F, H)
+        if cfg.activation == ACT_SITU:
+            R.situ_bf16(a, g, u, n * F, ctypes.c_float(cfg.beta), ctypes.c_float(cfg.linear_beta))
+        else:
+            assert ops.k3_rocm_swiglu_bf16(a, g, u, n * F)
+        R.mxfp4_gemm_bf16(yo, dp, ds, a, n, H, F)
+        R.scatter_rows_bf16(slots, yo, route_d[o:o + n], n, H)
+    c = torch.zeros((T, H), dtype=torch.bfloat16, device=cuda)
+    out = torch.zeros_like(c)
+    R.weighted_sum_bf16_batch(c, slots, w, T, k, H)
+    R.add_bf16(out, r, c, T * H)
+    sync()
+    return L.bf16_bits(out), ids_h, w.cpu().numpy()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("cfg,T", [(CONFIGS[2], 64), (CONFIGS[3], 512), (K3_NATIVE, 64)],
+                         ids=lambda v: getattr(v, "name", str(v)))
+def test_prefill_vs_reference_composition(cuda, cfg, T):
+    """The layer on token batches (exact and MFMA precisions) against the
+    reference's prefill composition on the same inputs. Exact: the bar of
+    the decode comparison. MFMA (two-term MXFP8 activations): rel-L2 <=
+    5e-3 and every element within 6 bf16 ulp of max(|ref|, output RMS)
+    (the MFMA path's own bound against the exact path, 4 ulp, plus the
+    exact path's 2 ulp against the reference)."""
+    inputs = make_inputs(cfg, tokens=T)
+    moe = get_layer(cfg, inputs, cuda)
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    want, ir, wr = reference_prefill(cfg, moe, x, r, cuda)
+    for precision in (0, 1):
+        ids = torch.zeros((T, cfg.top_k), dtype=torch.int32, device=cuda)
+        w = torch.zeros((T, cfg.top_k), dtype=torch.float32, device=cuda)
+        out = moe.forward(x, r, ids=ids, weights=w, precision=precision)
+        sync()
+        got, im = L.bf16_bits(out), u32(ids)
+        bad = route_mismatches(ir, im, inputs, cfg.top_k)
+        same = np.setdiff1d(np.arange(T), bad)
+        np.testing.assert_allclose(w.cpu().numpy()[same], wr[same], rtol=0, atol=1e-6 * cfg.scale)
+        label = f"{cfg.name} T={T} {'exact' if precision == 0 else 'mfma'} vs reference prefill"
+        if precision == 0:
+            check_outputs(got[same], want[same], label)
+        else:
+            g = bf16_bits_to_f32(got[same]).astype(np.float64)
+            f = bf16_bits_to_f32(want[same]).astype(np.float64)
+            rel = np.linalg.norm(g - f) / np.linalg.norm(f)
+            rms = float(np.sqrt(np.mean(f * f)))
+            worst = float((np.abs(g - f) / ulp_bf16(np.maximum(np.abs(f), rms))).max())
+            print(f"\n{label}: {bad.size} route near-ties, rel-L2 {rel:.3g}, worst {worst:.2f} ulp")
+            assert rel <= 5e-3
+            assert worst <= 6
