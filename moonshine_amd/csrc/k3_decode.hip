@@ -74,8 +74,8 @@ __global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
     for (int j = 0; j < kRouterMaxChunks; j++) {
         /* out-of-range chunks load chunk 0 and are skipped below */
         const uint32_t c = lane + 64u * j < chunks ? lane + 64u * j : 0u;
-        wa[j] = w0[c];
-        wb[j] = w1[c];
+        wa[j] = gload_nt(w0 + c);
+        wb[j] = gload_nt(w1 + c);
         xv[j] = x4[c];
     }
     float a = 0.0f, b = 0.0f;
@@ -207,8 +207,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
         const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)(row0 + srow0) * (H / 2u) + 16u * g;
 #pragma unroll
         for (int i = 0; i < kGU; i++) {
-            w[i] = gload16(gp + (uint64_t)i * (H / 2u), a16);
-            w[kGU + i] = gload16(up + (uint64_t)i * (H / 2u), a16);
+            w[i] = gload16_nt(gp + (uint64_t)i * (H / 2u), a16);
+            w[kGU + i] = gload16_nt(up + (uint64_t)i * (H / 2u), a16);
         }
     }
     if (words) {
@@ -216,8 +216,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(DecodeParams P) {
         for (int k = 0; k < 2; k++) {
             const uint32_t d = t + 256u * (uint32_t)k;
             if (d < nd) {
-                sw[k] = *(const __attribute__((address_space(1))) uint32_t *)(gs + 4u * d);
-                sw[2 + k] = *(const __attribute__((address_space(1))) uint32_t *)(us + 4u * d);
+                sw[k] = gload_nt((const uint32_t *)(gs + 4u * d));
+                sw[2 + k] = gload_nt((const uint32_t *)(us + 4u * d));
             }
         }
     }
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
         if (lane + 64u * m < G) {
 #pragma unroll
             for (int i = 0; i < RB; i++)
-                w[m][i] = gload16(dp + (uint64_t)i * (F / 2u) + 16u * (lane + 64u * m), a16);
+                w[m][i] = gload16_nt(dp + (uint64_t)i * (F / 2u) + 16u * (lane + 64u * m), a16);
         }
     }
     uint4 xa[M];
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void down_kernel(DecodeParams P) {
         const uint32_t *dw = (const uint32_t *)ds;
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            if (4u * (lane + 64u * k) < nbytes) sw[k] = *(const __attribute__((address_space(1))) uint32_t *)(dw + lane + 64u * k);
+            if (4u * (lane + 64u * k) < nbytes) sw[k] = gload_nt(dw + lane + 64u * k);
     }
 #pragma unroll
     for (int k = 0; k < M; k++) {

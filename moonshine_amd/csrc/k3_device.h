@@ -41,6 +41,24 @@ __device__ __forceinline__ uint4 gload16(const uint8_t *p, bool a16) {
     const uint2 lo = ((const uint2 *)p)[0], hi = ((const uint2 *)p)[1];
     return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
+/* Streaming forms for weights read once per call (decode): the
+ * non-temporal hint keeps a layer's ~0.4 GB expert stream from allocating
+ * in the L2 and the last-level cache (measured: decode layer 84.6 -> 80.5
+ * us). */
+__device__ __forceinline__ uint4 gload_nt(const uint4 *p) {
+    const u32x4_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 gload16_nt(const uint8_t *p, bool a16) {
+    if (a16) return gload_nt((const uint4 *)p);
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    const __attribute__((address_space(1))) u32x2_t *q = (const __attribute__((address_space(1))) u32x2_t *)p;
+    const u32x2_t lo = __builtin_nontemporal_load(q), hi = __builtin_nontemporal_load(q + 1);
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+__device__ __forceinline__ uint32_t gload_nt(const uint32_t *p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint32_t *)p);
+}
 __device__ __forceinline__ uint32_t gload(const uint8_t *p) {
     return *(const __attribute__((address_space(1))) uint8_t *)p;
 }
