@@ -195,7 +195,7 @@ struct Deal {
     static_assert(partial || N % W == 0, "chunks split evenly over the waves");
 };
 
-template <int MW_, int NW_, int WM_, int WN_, int TERMS_, int STAGES_, int KS_ = 1>
+template <int MW_, int NW_, int WM_, int WN_, int TERMS_, int STAGES_, int KS_ = 1, int BAUX_ = 0>
 struct TileCfg {
     static constexpr int MW = MW_, NW = NW_, WM = WM_, WN = WN_, TERMS = TERMS_;
     static constexpr int STAGES = STAGES_, NWV = MW * NW, THREADS = 64 * NWV;
@@ -204,6 +204,10 @@ struct TileCfg {
      * (8 rows each, the A layout); KS = 1 keeps the 16-row lane-order
      * fragments of 64 bytes per row. */
     static constexpr int KS = KS_, KSTEP = 128 * KS;
+    /* cache policy of the weight DMA (2 = non-temporal): classes whose
+     * experts own a single tile read every weight byte once per launch, so
+     * streaming them past L2 keeps the activations resident */
+    static constexpr int BAUX = BAUX_;
     static constexpr int BM = MW * 16 * WM, BN = NW * 16 * WN;
     static constexpr int A_CH = KS * TERMS * (BM / 16) * 2, B_CH = KS == 2 ? BN / 8 : BN / 16;
     /* E8M0 scales live outside the stages, in two scale buffers: a scale
@@ -237,12 +241,12 @@ struct TileCfg {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int Bytes>
+template <int Bytes, int Aux = 0>
 __device__ __forceinline__ void dma(const uint8_t *src, uint8_t *lds) {
     if constexpr (Bytes == 16)
-        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)lds, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)lds, 16, 0, Aux);
     else
-        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)lds, 4, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)lds, 4, 0, Aux);
 }
 
 /* s_waitcnt vmcnt(N) (N < 64), other counters untouched. */
@@ -302,7 +306,7 @@ __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, u
     if (L.mask & 4u) {
 #pragma unroll
         for (int q = 0; q < C::DB::per; q++)
-            dma<16>(L.b[q] + (uint32_t)(C::KSTEP / 2) * s, stage + C::OFF_B + 1024 * chunk_of<typename C::DB, W>(q, wave));
+            dma<16, C::BAUX>(L.b[q] + (uint32_t)(C::KSTEP / 2) * s, stage + C::OFF_B + 1024 * chunk_of<typename C::DB, W>(q, wave));
     }
 }
 
@@ -858,11 +862,11 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
  * blocks per CU; cfg2 gate/up 1.68 -> 1.60 ms, cfg3 level); its down keeps
  * 256-row blocks of four waves (measured 3% faster there). */
 template <int TERMS>
-using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2>;
+using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2, 2>;
 template <int TERMS>
-using Cls0G = TileCfg<1, 2, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2>;
+using Cls0G = TileCfg<1, 2, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2, 2>;
 template <int TERMS>
-using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2>;
+using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2, 2>;
 /* 128 x 512 blocks: eight waves, two per SIMD, each 64 activation rows x
  * 128 weight rows; halves the activation re-reads of a 256-wide block, two
  * stage buffers */
