@@ -65,10 +65,9 @@ __device__ __forceinline__ uint32_t gload(const uint8_t *p) {
 
 /* Round to nearest even; NaN stays a quiet NaN (hip_bfloat16 semantics). */
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t nan = (u >> 16) | 0x40u, rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? nan : rne); /* a select, no branch */
 }
 
 /* OCP E8M0 as the reference decodes it: 2^(e-127); 0 -> 2^-127 (bit pattern
@@ -83,11 +82,12 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
  * scaling). The CPU oracle evaluates the same sequence.
  */
 __device__ __forceinline__ float det_expf(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_huge_valf();
-    if (x < -103.97208404541015625f) return 0.0f;
-    const float n = rintf(__fmul_rn(x, 1.44269502162933349609375f));
-    float r = fmaf(-n, 0.693145751953125f, x);
+    /* the polynomial runs on x clamped into range (x itself wherever its
+     * value is used) and the special cases are selected at the end, so the
+     * sequence has no branches */
+    const float xc = fminf(fmaxf(x, -104.0f), 89.0f);
+    const float n = rintf(__fmul_rn(xc, 1.44269502162933349609375f));
+    float r = fmaf(-n, 0.693145751953125f, xc);
     r = fmaf(-n, 1.428606765330187045037746429443359375e-6f, r);
     float p = 1.9841270113736391067504882812e-4f;
     p = fmaf(p, r, 1.3888889225199818611145019531e-3f);
@@ -100,8 +100,11 @@ __device__ __forceinline__ float det_expf(float x) {
     const int ni = (int)n;
     const int a = ni / 2;
     const int b = ni - a;
-    return __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(a + 127) << 23)),
-                     __uint_as_float((uint32_t)(b + 127) << 23));
+    const float e = __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(a + 127) << 23)),
+                              __uint_as_float((uint32_t)(b + 127) << 23));
+    const float big = x > 88.72283935546875f ? __builtin_huge_valf() : e;
+    const float out = x < -103.97208404541015625f ? 0.0f : big;
+    return x != x ? x : out;
 }
 
 __device__ __forceinline__ float det_tanhf(float y) {
@@ -299,17 +302,76 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
     return sign | (uint32_t)(((ee + 7) << 3) | mant);
 }
 
+/* Two values to E4M3 codes in bytes 2 Hi .. 2 Hi + 1 of `old` (the other
+ * half kept), by the part's round-to-nearest-even conversion. For |v| <=
+ * 448 and non-NaN inputs it gives f32_to_e4m3's codes (pinned against the
+ * CPU encoder over every bf16 value within +-448, which covers every input
+ * the MXFP8 split produces: bf16 values scaled by powers of two and their
+ * residuals); NaN inputs are mapped to 0x7f as f32_to_e4m3 does. */
+template <bool Hi>
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b, uint32_t old) {
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, Hi);
+    constexpr int sa = Hi ? 16 : 0;
+    if (a != a) w = (w & ~(0xffu << sa)) | (0x7fu << sa);
+    if (b != b) w = (w & ~(0xffu << (sa + 8))) | (0x7fu << (sa + 8));
+    return w;
+}
+
+/* e4m3x2 without the NaN mapping: a NaN input gives some E4M3 NaN code
+ * (0x7f or 0xff), for encoders whose NaN codes only need to decode as NaN. */
+template <bool Hi>
+__device__ __forceinline__ uint32_t e4m3x2_raw(float a, float b, uint32_t old) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, Hi);
+}
+
+/* Two values rounded to bf16 (nearest even) by the part's packed
+ * conversion, back as fp32; f32_to_bf16's values except that a NaN's
+ * payload is not specified. */
+__device__ __forceinline__ float2 bf16r2(float a, float b) {
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    typedef float f32x2_v __attribute__((ext_vector_type(2)));
+    const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_v{a, b}, bf16x2_v));
+    return make_float2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
+
+/* Byte Sel of w as E4M3, decoded exactly (e4m3_to_f32's values). */
+template <int Sel>
+__device__ __forceinline__ float e4m3_byte(uint32_t w) {
+    return __builtin_amdgcn_cvt_f32_fp8((int)w, Sel);
+}
+
+/* DPP lane read within a 16-lane row (all lanes active). */
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xf, 0xf, false));
+}
+
+/* Maximum over each aligned group of N lanes (N = 8 or 16) of a 16-lane
+ * row, returned to every lane of the group: swaps of neighbours and of
+ * pairs, then the mirror inside 8 lanes and (N = 16) inside the row.
+ * fmaxf ignores NaN, so the result does not depend on the order. */
+template <int N>
+__device__ __forceinline__ float row_group_max(float v) {
+    static_assert(N == 8 || N == 16, "8- or 16-lane groups");
+    v = fmaxf(v, dpp_f<0xb1>(v));  /* quad_perm [1,0,3,2] */
+    v = fmaxf(v, dpp_f<0x4e>(v));  /* quad_perm [2,3,0,1] */
+    v = fmaxf(v, dpp_f<0x141>(v)); /* row_half_mirror */
+    if constexpr (N == 16) v = fmaxf(v, dpp_f<0x140>(v)); /* row_mirror */
+    return v;
+}
+
 /* Block exponent for MXFP8: floor(log2(amax)) - 8, plus one when the
  * maximum would exceed 448 after scaling, clamped to >= -127; -127 for an
  * all-zero block. Returns the scale byte (X + 127). */
 __device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
-    int X = -127;
-    if (amax > 0.0f) {
-        X = ilog2_pos(amax) - 8;
-        if (__fmul_rn(amax, __uint_as_float((uint32_t)(127 - X) << 23)) > 448.0f) X++;
-        if (X < -127) X = -127;
-    }
-    return (uint32_t)(X + 127);
+    /* for a normal amax = 1.m 2^(e - 127): X = e - 135, and amax 2^-X =
+     * 256 x 1.m exceeds 448 exactly when 1.m > 1.75 (mantissa field above
+     * 0x600000), or for +inf; zero, subnormal and amax < 2^-119 clamp to
+     * X = -127, i.e. byte 0 (branch-free) */
+    const uint32_t u = __float_as_uint(amax);
+    const int e = (int)((u >> 23) & 255u);
+    const int b = e - 8 + (((u & 0x7fffffu) > 0x600000u || e == 255) ? 1 : 0);
+    return amax > 0.0f && b > 0 ? (uint32_t)b : 0u;
 }
 
 /* 2^-(byte - 127) as the multiplier applied before rounding to E4M3. */

@@ -63,13 +63,14 @@ __global__ __launch_bounds__(256) void x_split_kernel(MfmaBuffers B, const uint1
         uint32_t w[8];
 #pragma unroll
         for (int q = 0; q < 8; q++) {
-            uint32_t word = 0u;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t code = f32_to_e4m3(__fmul_rn(v[4 * q + i], inv));
-                word |= code << (8 * i);
-                if (TERMS == 2 && t == 0)
-                    v[4 * q + i] = __fsub_rn(v[4 * q + i], __fmul_rn(e4m3_to_f32(code), sc));
+            float *u = v + 4 * q;
+            uint32_t word = e4m3x2<false>(__fmul_rn(u[0], inv), __fmul_rn(u[1], inv), 0u);
+            word = e4m3x2<true>(__fmul_rn(u[2], inv), __fmul_rn(u[3], inv), word);
+            if (TERMS == 2 && t == 0) {
+                u[0] = __fsub_rn(u[0], __fmul_rn(e4m3_byte<0>(word), sc));
+                u[1] = __fsub_rn(u[1], __fmul_rn(e4m3_byte<1>(word), sc));
+                u[2] = __fsub_rn(u[2], __fmul_rn(e4m3_byte<2>(word), sc));
+                u[3] = __fsub_rn(u[3], __fmul_rn(e4m3_byte<3>(word), sc));
             }
             w[q] = word;
         }
@@ -642,6 +643,93 @@ struct GateUpArgs {
 };
 
 /*
+ * Gate/up epilogue for activation kind KIND: lane (g, c) holds, for each of
+ * its rows, the gate and up sums of G = WN / 2 consecutive f-columns fw0 +
+ * G c + j. Each row's activation is rounded to bf16 and split into MXFP8
+ * terms per 32-column block (32 / G lanes of one DPP row: maximum by DPP),
+ * and each lane writes its G codes of a row and term with one store.
+ */
+template <class C, uint32_t KIND>
+__device__ __forceinline__ void gateup_epilogue(const f32x4 (&acc)[C::WM][C::WN],
+                                                const GateUpArgs &A, uint32_t row0, uint32_t rows,
+                                                uint32_t fw0, uint32_t wm, uint32_t g, uint32_t c) {
+    constexpr int G = C::WN / 2, LB = 32 / G;
+    static_assert(G == 2 || G == 4, "two or four columns per lane");
+    const uint32_t F = A.F;
+    /* template loops: the rows must unroll fully (acc indices constant)
+     * even where the activation's body exceeds the unroller's budget */
+    static_for<C::WM * 4>([&](auto IR) {
+            constexpr int i = decltype(IR)::value / 4, r = decltype(IR)::value % 4;
+            const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
+            const uint64_t prow = (uint64_t)row0 + (lr < rows ? lr : 0u);
+            float v[G];
+            if constexpr (KIND == 1u) {
+                /* SwiGLU g sigmoid(g) u with the sigmoid from the hardware
+                 * exp2 and reciprocal (each within 1 ulp): this path's
+                 * two-term split already carries ~2^-16 relative error,
+                 * and the value is rounded to bf16 first */
+#pragma unroll
+                for (int j = 0; j < G; j += 2) {
+                    const float2 gg = bf16r2(acc[i][j][r], acc[i][j + 1][r]);
+                    const float2 uu = bf16r2(acc[i][G + j][r], acc[i][G + j + 1][r]);
+                    const float g2[2] = {gg.x, gg.y}, u2[2] = {uu.x, uu.y};
+                    float h[2];
+#pragma unroll
+                    for (int k = 0; k < 2; k++) {
+                        const float e = __builtin_amdgcn_exp2f(__fmul_rn(g2[k], -1.44269502162933349609375f));
+                        const float sg = __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e));
+                        h[k] = __fmul_rn(__fmul_rn(g2[k], sg), u2[k]);
+                    }
+                    const float2 hh = bf16r2(h[0], h[1]);
+                    v[j] = hh.x;
+                    v[j + 1] = hh.y;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < G; j++) {
+                    v[j] = bf16r(gated_act(bf16r(acc[i][j][r]), bf16r(acc[i][G + j][r]), KIND,
+                                           A.beta, A.lb));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < C::TERMS; t++) {
+                float amax = fabsf(v[0]);
+#pragma unroll
+                for (int j = 1; j < G; j++) amax = fmaxf(amax, fabsf(v[j]));
+                amax = row_group_max<LB>(amax);
+                const uint32_t sbyte = mx8_scale_byte(amax);
+                const float inv = mx8_inv_scale(sbyte), sc = e8m0_to_f32(sbyte);
+                /* code x scale is exact (a 4-bit significand times a power
+                 * of two at or above 2^-127), so the residual is one fma */
+                uint32_t w = e4m3x2_raw<false>(__fmul_rn(v[0], inv), __fmul_rn(v[1], inv), 0u);
+                if constexpr (G == 4)
+                    w = e4m3x2_raw<true>(__fmul_rn(v[2], inv), __fmul_rn(v[3], inv), w);
+                if (C::TERMS == 2 && t == 0) {
+                    v[0] = fmaf(-e4m3_byte<0>(w), sc, v[0]);
+                    v[1] = fmaf(-e4m3_byte<1>(w), sc, v[1]);
+                    if constexpr (G == 4) {
+                        v[2] = fmaf(-e4m3_byte<2>(w), sc, v[2]);
+                        v[3] = fmaf(-e4m3_byte<3>(w), sc, v[3]);
+                    }
+                }
+                if (lr < rows) {
+                    uint8_t *dst = A.B.aq[t] + prow * F + fw0 + (uint32_t)G * c;
+                    if constexpr (G == 4)
+                        *(uint32_t *)dst = w;
+                    else
+                        *(uint16_t *)dst = (uint16_t)w;
+                    if (c % (uint32_t)LB == 0u)
+                        A.B.as[t][prow * (F / 32u) + fw0 / 32u + c / (uint32_t)LB] = (uint8_t)sbyte;
+                }
+            }
+            /* one row at a time: interleaving rows raises the register
+             * pressure past the 128-row class's budget */
+            __builtin_amdgcn_sched_barrier(0);
+    });
+}
+
+/*
  * grid xcd_grid(tile cap, F / (BN / 2)), block C::THREADS. The block's
  * BN weight rows are BN / 2 gate rows and the same up rows: wave column wn
  * owns f-columns f0 + 8 WN wn .. + 8 WN, n-subtiles j < WN / 2 gate and
@@ -649,7 +737,7 @@ struct GateUpArgs {
  * activation, then the MXFP8 split of each 32-column block (two gate
  * subtiles x 16 lanes).
  */
-template <class C>
+template <class C, uint32_t KIND>
 __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
     __shared__ __attribute__((aligned(16))) uint8_t sbuf0[C::SBUF], sbuf1[C::SBUF];
@@ -664,13 +752,17 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     const uint32_t H = A.H, F = A.F;
     const k3_moe_expert ex = A.experts[e];
     constexpr int FW = 8 * C::WN; /* f-columns per wave column */
+    constexpr int G = C::WN / 2;  /* gate (and up) columns per lane and row */
     const uint32_t f0 = colb * (uint32_t)(C::BN / 2);
     /* weight row of block subtile J, lane row c: gate rows for the first
-     * half of each wave column's subtiles, up rows (offset by F) after */
+     * half of each wave column's subtiles, up rows (offset by F) after.
+     * Lane row c of gate subtile j takes f-column G c + j, so each lane's
+     * accumulators hold G consecutive columns of every row (one packed
+     * store per row and term in the epilogue). */
     auto wrow = [&](int J, uint32_t cc) -> uint32_t {
         const int wcol = J / C::WN, j = J % C::WN;
-        const uint32_t f = f0 + (uint32_t)(FW * wcol) + 16u * (uint32_t)(j % (C::WN / 2)) + cc;
-        return j < C::WN / 2 ? f : F + f; /* rows >= F address the up tensor */
+        const uint32_t f = f0 + (uint32_t)(FW * wcol) + (uint32_t)G * cc + (uint32_t)(j % G);
+        return j < G ? f : F + f; /* rows >= F address the up tensor */
     };
     auto tok = [&](uint32_t r) -> uint32_t {
         return A.token_index[row0 + (r < rows ? r : 0u)];
@@ -733,41 +825,7 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, H, wm, wn, live_blocks<C>(rows, wm));
 
     const uint32_t fw0 = f0 + (uint32_t)FW * wn;
-#pragma unroll
-    for (int i = 0; i < C::WM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
-            const uint64_t prow = (uint64_t)row0 + (lr < rows ? lr : 0u);
-#pragma unroll
-            for (int q = 0; q < C::WN / 4; q++) { /* 32-column blocks */
-                float v[2];
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int jg = 2 * q + h;
-                    v[h] = bf16r(gated_act(bf16r(acc[i][jg][r]), bf16r(acc[i][C::WN / 2 + jg][r]),
-                                           A.kind, A.beta, A.lb));
-                }
-#pragma unroll
-                for (int t = 0; t < C::TERMS; t++) {
-                    float amax = fmaxf(fabsf(v[0]), fabsf(v[1]));
-#pragma unroll
-                    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-                    const uint32_t sbyte = mx8_scale_byte(amax);
-                    const float inv = mx8_inv_scale(sbyte), sc = e8m0_to_f32(sbyte);
-#pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const uint32_t code = f32_to_e4m3(__fmul_rn(v[h], inv));
-                        if (lr < rows)
-                            A.B.aq[t][prow * F + fw0 + 32u * q + 16u * h + c] = (uint8_t)code;
-                        if (C::TERMS == 2 && t == 0)
-                            v[h] = __fsub_rn(v[h], __fmul_rn(e4m3_to_f32(code), sc));
-                    }
-                    if (lr < rows && c == 0u)
-                        A.B.as[t][prow * (F / 32u) + fw0 / 32u + q] = (uint8_t)sbyte;
-                }
-            }
-        }
+    gateup_epilogue<C, KIND>(acc, A, row0, rows, fw0, wm, g, c);
 }
 
 /* ---------------------------------------------------------------------- */
@@ -802,6 +860,12 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     const uint32_t d0 = colb * (uint32_t)C::BN;
     const uint8_t *wp = (const uint8_t *)ex.down_packed, *ws = (const uint8_t *)ex.down_scales;
     auto prow = [&](uint32_t r) -> uint64_t { return (uint64_t)row0 + (r < rows ? r : 0u); };
+    /* output column of block subtile J, lane row cc: lane row cc of wave
+     * column w's subtile j takes column 16 WN w + WN cc + j, so each lane
+     * holds WN consecutive columns of every row (one store per row) */
+    auto dcol = [&](int J, uint32_t cc) -> uint32_t {
+        return d0 + (uint32_t)(16 * C::WN * (J / C::WN)) + (uint32_t)C::WN * cc + (uint32_t)(J % C::WN);
+    };
     Loader<C> L;
     constexpr int W = C::NWV;
     L.mask = kinds_held<C>(wave);
@@ -818,16 +882,16 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
         const int ch = min(chunk_of<typename C::DB, W>(q, wave), C::B_CH - 1);
         if constexpr (C::KS == 2) {
             const uint32_t h = (uint32_t)ch & 1u;
-            L.b[q] = wp + (uint64_t)(d0 + 16u * (uint32_t)(ch >> 1) + a_dma_row(lane, h)) * (F / 2u) +
+            L.b[q] = wp + (uint64_t)dcol(ch >> 1, a_dma_row(lane, h)) * (F / 2u) +
                      16u * a_dma_piece(lane, h);
         } else {
-            L.b[q] = wp + (uint64_t)(d0 + 16u * ch + c) * (F / 2u) + 16u * g;
+            L.b[q] = wp + (uint64_t)dcol(ch, c) * (F / 2u) + 16u * g;
         }
     }
 #pragma unroll
     for (int q = 0; q < C::DSB::per; q++) {
         const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
-        L.sb[q] = ws + (uint64_t)(d0 + 64u * ch + lane) * (F / 32u);
+        L.sb[q] = ws + (uint64_t)dcol(4 * ch + (int)g, c) * (F / 32u);
     }
 #pragma unroll
     for (int q = 0; q < C::DSA::per; q++) {
@@ -849,10 +913,17 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
             const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
             if (lr >= rows) continue;
             const uint64_t route = A.route_index[row0 + lr];
+            static_assert(C::WN == 4 || C::WN == 8, "four or eight columns per lane");
+            uint32_t pk[C::WN / 2];
 #pragma unroll
-            for (int j = 0; j < C::WN; j++)
-                A.y[route * H + d0 + 16u * (wn * C::WN + (uint32_t)j) + c] =
-                    f32_to_bf16(acc[i][j][r]);
+            for (int j = 0; j < C::WN / 2; j++)
+                pk[j] = (uint32_t)f32_to_bf16(acc[i][2 * j][r]) |
+                        ((uint32_t)f32_to_bf16(acc[i][2 * j + 1][r]) << 16);
+            uint16_t *dst = A.y + route * H + d0 + 16u * C::WN * wn + (uint32_t)C::WN * c;
+            if constexpr (C::WN == 8)
+                *(uint4 *)dst = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            else
+                *(uint2 *)dst = make_uint2(pk[0], pk[1]);
         }
 }
 
@@ -875,8 +946,13 @@ using Cls2 = TileCfg<2, 4, 4, 8, TERMS, 2>;
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C>), dim3(xcd_grid(cap, a.F / (C::BN / 2))),
-                       dim3(C::THREADS), 0, st, a);
+    /* one kernel per activation kind: a kernel holding both epilogues runs
+     * out of registers in the 128-row class */
+    const dim3 grid(xcd_grid(cap, a.F / (C::BN / 2))), block(C::THREADS);
+    if (a.kind == 1u)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C, 1u>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma_kernel<C, 0u>), grid, block, 0, st, a);
 }
 
 template <class C>

@@ -82,6 +82,16 @@ def test_mx8_quantize_bitexact(cuda):
     x[32:64] = 1e-39
     x[64:96] = np.float32(6.5e4) * rng.standard_normal(32).astype(np.float32)
     xb = f32_to_bf16_bits(x)
+    # every bf16 value within +-448, 31 to a block behind a 448 marker (block
+    # scale 2^0, so each value is encoded as itself): every input the split
+    # can hand the E4M3 conversion is such a value times a power of two
+    pos = np.arange(0x0000, 0x43E1, dtype=np.uint32)
+    sweep = np.concatenate([pos, pos | 0x8000]).astype(np.uint16)
+    pad = (-sweep.size) % 31
+    sweep = np.concatenate([sweep, np.zeros(pad, np.uint16)]).reshape(-1, 31)
+    marker = np.full((sweep.shape[0], 1), 0x43E0, np.uint16)
+    xb = np.concatenate([xb, np.concatenate([marker, sweep], axis=1).ravel()])
+    n = xb.size
     src = torch.from_numpy(xb.view(np.int16)).to(cuda)
     hq = torch.empty(n, dtype=torch.uint8, device=cuda)
     lq = torch.empty(n, dtype=torch.uint8, device=cuda)
