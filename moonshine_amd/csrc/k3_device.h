@@ -303,22 +303,26 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
 }
 
 /* Two values to E4M3 codes in bytes 2 Hi .. 2 Hi + 1 of `old` (the other
- * half kept), by the part's round-to-nearest-even conversion. For |v| <=
- * 448 and non-NaN inputs it gives f32_to_e4m3's codes (pinned against the
- * CPU encoder over every bf16 value within +-448, which covers every input
- * the MXFP8 split produces: bf16 values scaled by powers of two and their
- * residuals); NaN inputs are mapped to 0x7f as f32_to_e4m3 does. */
+ * half kept), by the part's round-to-nearest-even conversion: f32_to_e4m3's
+ * codes for every input. Magnitudes are clamped to 448 first (only +-inf
+ * exceeds it after MXFP8 scaling) and NaN inputs are mapped to 0x7f, as
+ * f32_to_e4m3 does; the conversion itself is pinned against the CPU
+ * encoder over every bf16 value within +-448, which covers every input the
+ * MXFP8 split produces (bf16 values scaled by powers of two, and their
+ * residuals). */
 template <bool Hi>
 __device__ __forceinline__ uint32_t e4m3x2(float a, float b, uint32_t old) {
-    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, Hi);
+    const float ac = fminf(fmaxf(a, -448.0f), 448.0f), bc = fminf(fmaxf(b, -448.0f), 448.0f);
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ac, bc, (int)old, Hi);
     constexpr int sa = Hi ? 16 : 0;
     if (a != a) w = (w & ~(0xffu << sa)) | (0x7fu << sa);
     if (b != b) w = (w & ~(0xffu << (sa + 8))) | (0x7fu << (sa + 8));
     return w;
 }
 
-/* e4m3x2 without the NaN mapping: a NaN input gives some E4M3 NaN code
- * (0x7f or 0xff), for encoders whose NaN codes only need to decode as NaN. */
+/* e4m3x2 without the clamp and the NaN mapping, for encoders whose inputs
+ * are finite (within +-448 after scaling) or whose non-finite inputs only
+ * need to decode as NaN (an E4M3 NaN code, 0x7f or 0xff, may result). */
 template <bool Hi>
 __device__ __forceinline__ uint32_t e4m3x2_raw(float a, float b, uint32_t old) {
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, Hi);

@@ -81,6 +81,11 @@ def test_mx8_quantize_bitexact(cuda):
     x[:32] = 0.0
     x[32:64] = 1e-39
     x[64:96] = np.float32(6.5e4) * rng.standard_normal(32).astype(np.float32)
+    x[96:128] = rng.standard_normal(32).astype(np.float32)   # +-inf among finite values
+    x[100], x[113] = np.inf, -np.inf
+    x[128:160] = rng.standard_normal(32).astype(np.float32)  # NaN among finite values
+    x[130] = np.nan
+    x[160:192] = np.float32(2.0 ** -133)                      # amax below 2^-119: scale byte 0
     xb = f32_to_bf16_bits(x)
     # every bf16 value within +-448, 31 to a block behind a 448 marker (block
     # scale 2^0, so each value is encoded as itself): every input the split
