@@ -326,6 +326,22 @@ bool k3_moe_native_forward_bf16(void *output, const void *hidden, const void *re
                                 void *shared_stream);
 
 /*
+ * The K3-native block's token-batch projection at the MXFP8 precisions, on
+ * bf16 MFMA. No counterpart in the reference (its projections are the VALU
+ * row kernels behind k3_rocm_q8_128_gemm_bf16 / k3_rocm_bf16_gemm_bf16);
+ * exposed for callers that want the MFMA form directly and for its tests.
+ *   q8:  output[t, r] = bf16(sum_b scales[r, b] sum_{k in block b} q[r, k] input[t, k])
+ *   bf16 weights: output[t, r] = bf16(sum_k w[r, k] input[t, k])
+ * Every product is exact (int8 codes are exact in bf16); only the fp32
+ * summation order differs from the row kernels. columns % 128 == 0 (q8) or
+ * % 64 == 0, input 16-byte and weights 8-byte (q8) or 16-byte aligned,
+ * both operands under 2 GiB; false otherwise.
+ */
+bool k3_moe_proj_mfma_bf16(void *output, const void *weights, const float *scales,
+                           const void *input, uint32_t vector_count, uint32_t rows,
+                           uint32_t columns, bool q8, void *stream);
+
+/*
  * Synthetic resident expert store for benchmarks and tests: fills `bytes`
  * of device memory at `base` with the counter-based generator
  * k3_moe_synth_byte(seed, stream, index) below. Packed tensors use uniform

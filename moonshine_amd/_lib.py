@@ -122,6 +122,7 @@ SIGNATURES = {
     "k3_moe_router_choices_f32": (_b, [_p, _p, _p, _u32, _u32, _p]),
     "k3_moe_experts_bf16": (_b, [_p, _p, _p, _p, _p, _p, ctypes.POINTER(K3MoeShape), _u32,
                                  _u32, _p, _sz, _p]),
+    "k3_moe_proj_mfma_bf16": (_b, [_p, _p, _p, _p, _u32, _u32, _u32, ctypes.c_bool, _p]),
     "k3_moe_synth_fill": (_b, [_p, _u64, _u64, _u64, _u32, _p]),
     "k3_moe_synth_fill_host": (None, [_p, _u64, _u64, _u64, _u32]),
     "k3_moe_mx8_quantize_bf16": (_b, [_p, _p, _p, _p, _p, _u64, _p]),

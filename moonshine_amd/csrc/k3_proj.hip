@@ -247,3 +247,11 @@ bool launch_proj_mfma(uint16_t *out, const void *x, const void *weights, const f
 }
 
 }  // namespace k3
+
+extern "C" bool k3_moe_proj_mfma_bf16(void *output, const void *weights, const float *scales,
+                                      const void *input, uint32_t vector_count, uint32_t rows,
+                                      uint32_t columns, bool q8, void *stream) {
+    if (!output || !weights || !input) return false;
+    return k3::launch_proj_mfma((uint16_t *)output, input, weights, scales, vector_count, rows,
+                                columns, q8, (hipStream_t)stream);
+}

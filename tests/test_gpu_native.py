@@ -157,3 +157,59 @@ def test_native_graph_replay_same_bits(cuda, streams):
         eager = layer.forward(dx[2], dr[2])  # eager work on the same workspace
         torch.cuda.synchronize()
         np.testing.assert_array_equal(bf16_bits(eager), want[2])
+
+
+@pytest.mark.parametrize("q8", [True, False])
+@pytest.mark.parametrize("T,rows,cols", [(1, 200, 384), (33, 200, 384), (130, 129, 1024),
+                                         (256, 256, 512)])
+def test_proj_mfma_ragged_vs_row_kernels(cuda, q8, T, rows, cols):
+    """k3_moe_proj_mfma_bf16 at ragged token and row counts (partial
+    128 x 128 tiles, clamped rows) against the exact row kernels. Each
+    output may differ from the row kernel's by the two fp32 summation
+    orders' error (at most 2 K u sum |products| between them, u = 2^-24)
+    plus one bf16 rounding step of the larger value; most elements are
+    identical."""
+    import ctypes
+    from moonshine_amd import ops
+    from moonshine_amd._lib import lib
+    rng = np.random.default_rng(T * 1000 + rows + cols + q8)
+    x = f32_to_bf16_bits(rng.normal(0, 1, (T, cols)).astype(np.float32))
+    xd = torch.from_numpy(x.view(np.int16)).to(cuda)
+    if q8:
+        q = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+        s = (rng.random((rows, cols // 128)) * 1e-2 + 1e-3).astype(np.float32)
+        wd, sd = torch.from_numpy(q).to(cuda), torch.from_numpy(s).to(cuda)
+        wf = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
+    else:
+        w = f32_to_bf16_bits(rng.normal(0, 0.05, (rows, cols)).astype(np.float32))
+        wd, sd = torch.from_numpy(w.view(np.int16)).to(cuda), None
+        wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    want = torch.zeros((T, rows), dtype=torch.int16, device=cuda)
+    got = torch.full((T, rows), -1, dtype=torch.int16, device=cuda)
+    if q8:
+        assert ops.k3_rocm_q8_128_gemm_bf16(want, wd, sd, xd, T, rows, cols)
+    else:
+        assert ops.k3_rocm_bf16_gemm_bf16(want, wd, xd, T, rows, cols)
+    P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib().k3_moe_proj_mfma_bf16(P(got), P(wd), P(sd), P(xd), T, rows, cols, q8, st)
+    torch.cuda.synchronize()
+    g = (got.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    e = (want.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    absum = np.abs(xf) @ np.abs(wf).T                      # sum |products| per output
+    exact = xf @ wf.T
+    m = np.maximum(np.abs(g), np.abs(e))
+    ulp = np.ldexp(1.0, np.floor(np.log2(np.maximum(m, 1e-30))).astype(int) - 7)
+    bound = 2.0 * cols * 2.0 ** -24 * absum + ulp
+    d = np.abs(g - e)
+    assert np.all(d <= bound), f"worst excess {np.max(d - bound):.3g}"
+    # both near the fp64 value (a wrong row, scale or clamp is far outside)
+    assert np.all(np.abs(g - exact) <= bound + np.abs(exact) * 2.0 ** -8)
+    same = np.mean(d == 0)
+    print(f"T={T} rows={rows} cols={cols} q8={q8}: identical {same:.1%}, worst |d|/ulp {np.max(d / ulp):.2f}")
+    assert same >= 0.5
+    # argument checks
+    assert not lib().k3_moe_proj_mfma_bf16(P(got), P(wd), P(sd), P(xd), T, rows, cols - 32, q8, st)
+    if q8:
+        assert not lib().k3_moe_proj_mfma_bf16(P(got), P(wd), None, P(xd), T, rows, cols, q8, st)
