@@ -48,11 +48,10 @@ K3_NATIVE = Config("k3-native", 1, 3584, 896, 16, 3072, scale=1.0, activation=AC
 
 def f32_to_bf16_bits(a):
     """float32 -> bf16 bit patterns (uint16), round to nearest even."""
-    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = np.asarray(a, dtype=np.float32, order="C").view(np.uint32).astype(np.uint64)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
-    return r
+    r = np.where(nan, (u >> 16) | 0x40, (u + 0x7FFF + ((u >> 16) & 1)) >> 16)
+    return np.asarray(r, dtype=np.uint16)
 
 
 def bf16_bits_to_f32(b):
