@@ -657,73 +657,73 @@ __device__ __forceinline__ void gateup_epilogue(const f32x4 (&acc)[C::WM][C::WN]
     /* template loops: the rows must unroll fully (acc indices constant)
      * even where the activation's body exceeds the unroller's budget */
     static_for<C::WM * 4>([&](auto IR) {
-            constexpr int i = decltype(IR)::value / 4, r = decltype(IR)::value % 4;
-            const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
-            const uint64_t prow = (uint64_t)row0 + (lr < rows ? lr : 0u);
-            float v[G];
-            if constexpr (KIND == 1u) {
-                /* SwiGLU g sigmoid(g) u with the sigmoid from the hardware
-                 * exp2 and reciprocal (each within 1 ulp): this path's
-                 * two-term split already carries ~2^-16 relative error,
-                 * and the value is rounded to bf16 first */
+        constexpr int i = decltype(IR)::value / 4, r = decltype(IR)::value % 4;
+        const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
+        const uint64_t prow = (uint64_t)row0 + (lr < rows ? lr : 0u);
+        float v[G];
+        if constexpr (KIND == 1u) {
+            /* SwiGLU g sigmoid(g) u with the sigmoid from the hardware
+             * exp2 and reciprocal (each within 1 ulp): this path's
+             * two-term split already carries ~2^-16 relative error,
+             * and the value is rounded to bf16 first */
 #pragma unroll
-                for (int j = 0; j < G; j += 2) {
-                    const float2 gg = bf16r2(acc[i][j][r], acc[i][j + 1][r]);
-                    const float2 uu = bf16r2(acc[i][G + j][r], acc[i][G + j + 1][r]);
-                    const float g2[2] = {gg.x, gg.y}, u2[2] = {uu.x, uu.y};
-                    float h[2];
+            for (int j = 0; j < G; j += 2) {
+                const float2 gg = bf16r2(acc[i][j][r], acc[i][j + 1][r]);
+                const float2 uu = bf16r2(acc[i][G + j][r], acc[i][G + j + 1][r]);
+                const float g2[2] = {gg.x, gg.y}, u2[2] = {uu.x, uu.y};
+                float h[2];
 #pragma unroll
-                    for (int k = 0; k < 2; k++) {
-                        const float e = __builtin_amdgcn_exp2f(__fmul_rn(g2[k], -1.44269502162933349609375f));
-                        const float sg = __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e));
-                        h[k] = __fmul_rn(__fmul_rn(g2[k], sg), u2[k]);
-                    }
-                    const float2 hh = bf16r2(h[0], h[1]);
-                    v[j] = hh.x;
-                    v[j + 1] = hh.y;
+                for (int k = 0; k < 2; k++) {
+                    const float e = __builtin_amdgcn_exp2f(__fmul_rn(g2[k], -1.44269502162933349609375f));
+                    const float sg = __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e));
+                    h[k] = __fmul_rn(__fmul_rn(g2[k], sg), u2[k]);
                 }
-            } else {
+                const float2 hh = bf16r2(h[0], h[1]);
+                v[j] = hh.x;
+                v[j + 1] = hh.y;
+            }
+        } else {
 #pragma unroll
-                for (int j = 0; j < G; j++) {
-                    v[j] = bf16r(gated_act(bf16r(acc[i][j][r]), bf16r(acc[i][G + j][r]), KIND,
-                                           A.beta, A.lb));
-                    __builtin_amdgcn_sched_barrier(0);
+            for (int j = 0; j < G; j++) {
+                v[j] = bf16r(gated_act(bf16r(acc[i][j][r]), bf16r(acc[i][G + j][r]), KIND,
+                                       A.beta, A.lb));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < C::TERMS; t++) {
+            float amax = fabsf(v[0]);
+#pragma unroll
+            for (int j = 1; j < G; j++) amax = fmaxf(amax, fabsf(v[j]));
+            amax = row_group_max<LB>(amax);
+            const uint32_t sbyte = mx8_scale_byte(amax);
+            const float inv = mx8_inv_scale(sbyte), sc = e8m0_to_f32(sbyte);
+            /* code x scale is exact (a 4-bit significand times a power
+             * of two at or above 2^-127), so the residual is one fma */
+            uint32_t w = e4m3x2_raw<false>(__fmul_rn(v[0], inv), __fmul_rn(v[1], inv), 0u);
+            if constexpr (G == 4)
+                w = e4m3x2_raw<true>(__fmul_rn(v[2], inv), __fmul_rn(v[3], inv), w);
+            if (C::TERMS == 2 && t == 0) {
+                v[0] = fmaf(-e4m3_byte<0>(w), sc, v[0]);
+                v[1] = fmaf(-e4m3_byte<1>(w), sc, v[1]);
+                if constexpr (G == 4) {
+                    v[2] = fmaf(-e4m3_byte<2>(w), sc, v[2]);
+                    v[3] = fmaf(-e4m3_byte<3>(w), sc, v[3]);
                 }
             }
-#pragma unroll
-            for (int t = 0; t < C::TERMS; t++) {
-                float amax = fabsf(v[0]);
-#pragma unroll
-                for (int j = 1; j < G; j++) amax = fmaxf(amax, fabsf(v[j]));
-                amax = row_group_max<LB>(amax);
-                const uint32_t sbyte = mx8_scale_byte(amax);
-                const float inv = mx8_inv_scale(sbyte), sc = e8m0_to_f32(sbyte);
-                /* code x scale is exact (a 4-bit significand times a power
-                 * of two at or above 2^-127), so the residual is one fma */
-                uint32_t w = e4m3x2_raw<false>(__fmul_rn(v[0], inv), __fmul_rn(v[1], inv), 0u);
+            if (lr < rows) {
+                uint8_t *dst = A.B.aq[t] + prow * F + fw0 + (uint32_t)G * c;
                 if constexpr (G == 4)
-                    w = e4m3x2_raw<true>(__fmul_rn(v[2], inv), __fmul_rn(v[3], inv), w);
-                if (C::TERMS == 2 && t == 0) {
-                    v[0] = fmaf(-e4m3_byte<0>(w), sc, v[0]);
-                    v[1] = fmaf(-e4m3_byte<1>(w), sc, v[1]);
-                    if constexpr (G == 4) {
-                        v[2] = fmaf(-e4m3_byte<2>(w), sc, v[2]);
-                        v[3] = fmaf(-e4m3_byte<3>(w), sc, v[3]);
-                    }
-                }
-                if (lr < rows) {
-                    uint8_t *dst = A.B.aq[t] + prow * F + fw0 + (uint32_t)G * c;
-                    if constexpr (G == 4)
-                        *(uint32_t *)dst = w;
-                    else
-                        *(uint16_t *)dst = (uint16_t)w;
-                    if (c % (uint32_t)LB == 0u)
-                        A.B.as[t][prow * (F / 32u) + fw0 / 32u + c / (uint32_t)LB] = (uint8_t)sbyte;
-                }
+                    *(uint32_t *)dst = w;
+                else
+                    *(uint16_t *)dst = (uint16_t)w;
+                if (c % (uint32_t)LB == 0u)
+                    A.B.as[t][prow * (F / 32u) + fw0 / 32u + c / (uint32_t)LB] = (uint8_t)sbyte;
             }
-            /* one row at a time: interleaving rows raises the register
-             * pressure past the 128-row class's budget */
-            __builtin_amdgcn_sched_barrier(0);
+        }
+        /* one row at a time: interleaving rows raises the register
+         * pressure past the 128-row class's budget */
+        __builtin_amdgcn_sched_barrier(0);
     });
 }
 
@@ -731,9 +731,8 @@ __device__ __forceinline__ void gateup_epilogue(const f32x4 (&acc)[C::WM][C::WN]
  * grid xcd_grid(tile cap, F / (BN / 2)), block C::THREADS. The block's
  * BN weight rows are BN / 2 gate rows and the same up rows: wave column wn
  * owns f-columns f0 + 8 WN wn .. + 8 WN, n-subtiles j < WN / 2 gate and
- * j >= WN / 2 up, so gate and up of a column meet in one lane. Epilogue:
- * activation, then the MXFP8 split of each 32-column block (two gate
- * subtiles x 16 lanes).
+ * j >= WN / 2 up, so gate and up of a column meet in one lane (wrow gives
+ * each lane WN / 2 consecutive columns). Epilogue: gateup_epilogue.
  */
 template <class C, uint32_t KIND>
 __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
