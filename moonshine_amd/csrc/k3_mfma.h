@@ -21,18 +21,22 @@
 
 namespace k3 {
 
+/* Tile classes by an expert's row count: one 16-row tile (<= 16 rows), one
+ * 64-row tile (<= 64), one 96-row tile (<= 96), or 128-row tiles. */
+constexpr int kTileClasses = 4;
+
 struct MfmaBuffers {
     uint8_t *xq[2], *xs[2];     /* [T, H] codes, [T, H / 32] scales: hi, lo */
     uint8_t *aq[2], *as[2];     /* [routes, F] codes, [routes, F / 32] scales */
-    uint32_t *tiles;            /* 3 classes x tile_cap x {expert, row0, rows} */
-    uint32_t *tile_count;       /* [4] */
+    uint32_t *tiles;            /* kTileClasses x tile_cap x {expert, row0, rows} */
+    uint32_t *tile_count;       /* [kTileClasses] */
     uint32_t *unaligned;        /* [E + 1]: count, then the selected experts with a
                                    tensor that is not 16-byte aligned (any order) */
-    uint32_t tile_cap[3];
+    uint32_t tile_cap[kTileClasses];
 };
 
-/* Device tile bounds for T tokens (per class: 16-, 32- and 64-row tiles). */
-void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[3]);
+/* Device tile bounds for T tokens, per tile class. */
+void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[kTileClasses]);
 
 /* Plan (counts/offsets/unique/token_index/route_index) must be on the
  * stream already. Writes y [routes, H] bf16 in route order. terms: 1 or 2. */

@@ -37,7 +37,7 @@ namespace {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kTileRows[3] = {16u, 64u, 128u};
+constexpr uint32_t kTileRows[kTileClasses] = {16u, 64u, 96u, 128u};
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void x_split_kernel(MfmaBuffers B, const uint1
 
 /* One block of 1024 threads (thread e = expert e). Class 0: experts with
  * <= 16 rows (one 16-row tile), class 1: <= 64 rows (one 64-row tile),
- * class 2: 128-row tiles. Tiles are listed in expert order. An expert with
+ * class 2: <= 96 rows (one 96-row tile), class 3: 128-row tiles (the last
+ * one partial). Tiles are listed in expert order. An expert with
  * a tensor that is not 16-byte aligned (the 8-mod-16 starts of real
  * checkpoint spans) gets no tiles: direct-to-LDS loads move 16-byte
  * pieces, so B.unaligned[e] hands it to the exact grouped kernels. */
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
                                                           const uint32_t *__restrict__ offsets,
                                                           const k3_moe_expert *__restrict__ experts,
                                                           uint32_t E) {
-    __shared__ uint32_t wave_tot[3][16];
+    __shared__ uint32_t wave_tot[kTileClasses][16];
     __shared__ uint32_t odd_count;
     if (threadIdx.x == 0u) odd_count = 0u;
     __syncthreads();
@@ -110,25 +111,27 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
                16u) != 0u;
     }
     if (odd) B.unaligned[1u + atomicAdd(&odd_count, 1u)] = e;
-    const int cls = n == 0u || odd ? 3 : (n <= 16u ? 0 : (n <= 64u ? 1 : 2));
-    uint32_t nt[3], inc[3];
+    constexpr int kLast = kTileClasses - 1; /* the multi-tile class */
+    const int cls = n == 0u || odd ? kTileClasses
+                                   : (n <= 16u ? 0 : (n <= 64u ? 1 : (n <= 96u ? 2 : kLast)));
+    uint32_t nt[kTileClasses], inc[kTileClasses];
 #pragma unroll
-    for (int c = 0; c < 3; c++) {
-        nt[c] = cls == c ? (c == 2 ? (n + 127u) / 128u : 1u) : 0u;
+    for (int c = 0; c < kTileClasses; c++) {
+        nt[c] = cls == c ? (c == kLast ? (n + 127u) / 128u : 1u) : 0u;
         inc[c] = nt[c];
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1)
 #pragma unroll
-        for (int c = 0; c < 3; c++) {
+        for (int c = 0; c < kTileClasses; c++) {
             const uint32_t a = __shfl_up(inc[c], o, 64);
             if ((int)lane >= o) inc[c] += a;
         }
     if (lane == 63u)
-        for (int c = 0; c < 3; c++) wave_tot[c][wave] = inc[c];
+        for (int c = 0; c < kTileClasses; c++) wave_tot[c][wave] = inc[c];
     __syncthreads();
     uint32_t base_idx = 0u;
-    for (int c = 0; c < 3; c++) {
+    for (int c = 0; c < kTileClasses; c++) {
         uint32_t before = 0u, total = 0u;
         for (uint32_t w = 0; w < blockDim.x / 64u; w++) {
             if (w < wave) before += wave_tot[c][w];
@@ -216,7 +219,7 @@ struct TileCfg {
      * K), so a row's scales arrive in one 16-byte request per SQ stages
      * instead of a 4-byte request per stage. Chunk = 64 rows x 16 B. */
     static constexpr int SQ = 4 / KS;
-    static constexpr int SA_ROWS = BM < 64 ? 64 : BM;
+    static constexpr int SA_ROWS = (BM + 63) / 64 * 64; /* whole 64-row scale chunks */
     static constexpr int SA_CH = TERMS * SA_ROWS / 64, SB_CH = BN / 64;
     static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, STAGE = OFF_B + B_CH * 1024;
     static constexpr int OFF_SA = 0, OFF_SB = SA_CH * 1024, SBUF = (SA_CH + SB_CH) * 1024;
@@ -924,7 +927,7 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
         }
 }
 
-/* Tile classes (rows per tile): 16, 64, 128. One-term class 0 computes
+/* Tile classes (rows per tile): 16, 64, 96, 128. One-term class 0 computes
  * 32 rows so that its A chunks still split over the waves. Class 0's
  * gate/up takes 128-row weight blocks of two waves (80 KB of LDS: two
  * blocks per CU; cfg2 gate/up 1.68 -> 1.60 ms, cfg3 level); its down keeps
@@ -939,7 +942,17 @@ using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2, 2>;
  * 128 weight rows; halves the activation re-reads of a 256-wide block, two
  * stage buffers */
 template <int TERMS>
-using Cls2 = TileCfg<2, 4, 4, 8, TERMS, 2>;
+using Cls3 = TileCfg<2, 4, 4, 8, TERMS, 2>;
+/* 96 x 512 blocks for experts of 65-96 rows, one tile each (most experts
+ * of a Zipf batch's 128-row range): a quarter less activation staging per
+ * K step than a padded 128-row tile, 48 rows per wave. One term stages
+ * 12 activation chunks, which do not split over 8 waves: it keeps the
+ * 128-row blocks. */
+#ifndef K3_C2_AUX
+#define K3_C2_AUX 0
+#endif
+template <int TERMS>
+using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, K3_C2_AUX>, Cls3<TERMS>>;
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
@@ -974,38 +987,43 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
                   s.activation == 1u ? 1.0f : s.beta, s.activation == 1u ? 1.0f : s.linear_beta};
     DownArgs da{B, nullptr, nullptr, route_index, experts, y, H, F};
     uint32_t base = 0u;
-    const uint32_t *tl[3];
-    for (int c = 0; c < 3; c++) {
+    const uint32_t *tl[kTileClasses];
+    for (int c = 0; c < kTileClasses; c++) {
         tl[c] = B.tiles + 3u * base;
         base += B.tile_cap[c];
     }
-    for (int c = 0; c < 3; c++) {
+    for (int c = 0; c < kTileClasses; c++) {
         if (!B.tile_cap[c]) continue;
         ga.tiles = tl[c];
         ga.tile_count = B.tile_count + c;
         if (c == 0) launch_gateup<Cls0G<TERMS>>(ga, B.tile_cap[c], st);
         if (c == 1) launch_gateup<Cls1<TERMS>>(ga, B.tile_cap[c], st);
         if (c == 2) launch_gateup<Cls2<TERMS>>(ga, B.tile_cap[c], st);
+        if (c == 3) launch_gateup<Cls3<TERMS>>(ga, B.tile_cap[c], st);
     }
     mark(K3_MOE_STAGE_DOWN);
-    for (int c = 0; c < 3; c++) {
+    for (int c = 0; c < kTileClasses; c++) {
         if (!B.tile_cap[c]) continue;
         da.tiles = tl[c];
         da.tile_count = B.tile_count + c;
         if (c == 0) launch_down<Cls0<TERMS>>(da, B.tile_cap[c], st);
         if (c == 1) launch_down<Cls1<TERMS>>(da, B.tile_cap[c], st);
         if (c == 2) launch_down<Cls2<TERMS>>(da, B.tile_cap[c], st);
+        if (c == 3) launch_down<Cls3<TERMS>>(da, B.tile_cap[c], st);
     }
     return hipGetLastError() == hipSuccess;
 }
 
 }  // namespace
 
-void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[3]) {
+void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[kTileClasses]) {
     const uint64_t R = (uint64_t)T * k;
-    caps[0] = (uint32_t)(R < E ? R : E);
-    caps[1] = (uint32_t)(R / 17u < E ? R / 17u : E);
-    caps[2] = (uint32_t)(R / 128u + (R / 65u < E ? R / 65u : E));
+    auto upto = [&](uint64_t v) { return (uint32_t)(v < E ? v : E); };
+    caps[0] = upto(R);         /* experts with 1-16 rows */
+    caps[1] = upto(R / 17u);   /* 17-64 */
+    caps[2] = upto(R / 65u);   /* 65-96 */
+    /* > 96 rows: ceil(n / 128) <= n / 128 + 1 tiles each */
+    caps[3] = (uint32_t)(R / 128u) + upto(R / 97u);
 }
 
 bool mfma_supported(const k3_moe_shape &s) {

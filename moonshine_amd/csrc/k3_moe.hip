@@ -106,8 +106,10 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
             m.as[t] = take(1ull * routes * s.ffn / 32u);
         }
         mfma_tile_caps(T, s.top_k, s.expert_count, m.tile_cap);
-        m.tiles = (uint32_t *)take(12ull * (m.tile_cap[0] + m.tile_cap[1] + m.tile_cap[2]));
-        m.tile_count = (uint32_t *)take(16u);
+        uint64_t ntiles = 0u;
+        for (int c = 0; c < kTileClasses; c++) ntiles += m.tile_cap[c];
+        m.tiles = (uint32_t *)take(12ull * ntiles);
+        m.tile_count = (uint32_t *)take(4u * kTileClasses);
         m.unaligned = (uint32_t *)take(4ull * (s.expert_count + 1u));
     }
     w.bytes = off;
