@@ -167,3 +167,33 @@ def test_unsupported_shape_rejected(cuda):
     with pytest.raises(RuntimeError):
         forward(moe, inputs, cuda, MFMA)
     forward(moe, inputs, cuda, EXACT)  # the exact path takes any H % 32 == 0
+
+
+def test_tile_class_edges_vs_exact(cuda):
+    """Experts routed exactly 16, 17, 64, 65, 80, 96, 97, 128, 129 and 200
+    rows (every tile class and its edges, including the 96-row class and a
+    partial last 128-row tile), through k3_moe_experts_bf16 with given
+    routes: MFMA against the exact path (itself bit-exact to the oracle)."""
+    cfg = small_cfg(260)
+    inputs = make_inputs(cfg, tokens=cfg.tokens)
+    moe = get_layer(cfg, inputs, cuda)
+    T, k = cfg.tokens, cfg.top_k
+    counts = {0: 65, 1: 80, 2: 96, 3: 97, 4: 128, 5: 129, 6: 16, 7: 17, 8: 64, 9: 200}
+    ids = np.full((T, k), 0xFFFFFFFF, np.uint32)  # unused slots: no route
+    used = np.zeros(T, np.int64)
+    for e, n in counts.items():
+        order = np.argsort(used, kind="stable")[:n]  # the tokens with the fewest routes
+        for t in order:
+            ids[t, used[t]] = e
+            used[t] += 1
+    assert used.max() <= k
+    rng = np.random.default_rng(7)
+    w = (rng.random((T, k)) * 0.5 + 0.1).astype(np.float32)
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    ids_d = torch.from_numpy(ids.view(np.int32)).to(cuda)
+    w_d = torch.from_numpy(w).to(cuda)
+    out = moe.experts_only(x, ids_d, w_d, residual=r, precision=MFMA)
+    exact = moe.experts_only(x, ids_d, w_d, residual=r, precision=EXACT)
+    torch.cuda.synchronize()
+    assert_close(L.bf16_bits(out), L.bf16_bits(exact), "tile class edges mfma vs exact")
