@@ -35,6 +35,12 @@ struct MfmaBuffers {
     uint32_t tile_cap[kTileClasses];
 };
 
+/* Per-class tile lists of every selected expert (counts/offsets of the plan
+ * on the stream already), for the exact grouped kernels: tiles of at most
+ * 128 rows spread a heavy expert's rows over many workgroups. E <= 1024. */
+bool build_tiles_all(const MfmaBuffers &B, const uint32_t *counts, const uint32_t *offsets,
+                     const k3_moe_expert *experts, uint32_t E, hipStream_t st);
+
 /* Device tile bounds for T tokens, per tile class. */
 void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[kTileClasses]);
 

@@ -88,15 +88,17 @@ __global__ __launch_bounds__(256) void x_split_kernel(MfmaBuffers B, const uint1
 /* One block of 1024 threads (thread e = expert e). Class 0: experts with
  * <= 16 rows (one 16-row tile), class 1: <= 64 rows (one 64-row tile),
  * class 2: <= 96 rows (one 96-row tile), class 3: 128-row tiles (the last
- * one partial). Tiles are listed in expert order. An expert with
- * a tensor that is not 16-byte aligned (the 8-mod-16 starts of real
- * checkpoint spans) gets no tiles: direct-to-LDS loads move 16-byte
- * pieces, so B.unaligned[e] hands it to the exact grouped kernels. */
+ * one partial). Tiles are listed in expert order. For the MFMA kernels
+ * (all == 0) an expert with a tensor that is not 16-byte aligned (the
+ * 8-mod-16 starts of real checkpoint spans) gets no tiles: direct-to-LDS
+ * loads move 16-byte pieces, so B.unaligned hands it to the exact grouped
+ * kernels. With all != 0 (the exact kernels' own tile list) every selected
+ * expert gets tiles. */
 __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
                                                           const uint32_t *__restrict__ counts,
                                                           const uint32_t *__restrict__ offsets,
                                                           const k3_moe_expert *__restrict__ experts,
-                                                          uint32_t E) {
+                                                          uint32_t E, uint32_t all) {
     __shared__ uint32_t wave_tot[kTileClasses][16];
     __shared__ uint32_t odd_count;
     if (threadIdx.x == 0u) odd_count = 0u;
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
     const uint32_t e = threadIdx.x, lane = e & 63u, wave = e >> 6;
     const uint32_t n = e < E ? counts[e] : 0u;
     bool odd = false;
-    if (n != 0u) {
+    if (n != 0u && !all) {
         const k3_moe_expert ex = experts[e];
         odd = (((uintptr_t)ex.gate_packed | (uintptr_t)ex.gate_scales | (uintptr_t)ex.down_packed |
                 (uintptr_t)ex.down_scales | (uintptr_t)ex.up_packed | (uintptr_t)ex.up_scales) %
@@ -981,7 +983,7 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
     hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_kernel<TERMS>), dim3((uint32_t)((blocks + 255u) / 256u)),
                        dim3(256), 0, st, B, hidden, blocks);
     hipLaunchKernelGGL(tile_build_kernel, dim3(1), dim3(1024), 0, st, B, counts, offsets,
-                       experts, s.expert_count);
+                       experts, s.expert_count, 0u);
     mark(K3_MOE_STAGE_GATE_UP);
     GateUpArgs ga{B, nullptr, nullptr, token_index, experts, H, F, s.activation,
                   s.activation == 1u ? 1.0f : s.beta, s.activation == 1u ? 1.0f : s.linear_beta};
@@ -1024,6 +1026,14 @@ void mfma_tile_caps(uint32_t T, uint32_t k, uint32_t E, uint32_t caps[kTileClass
     caps[2] = upto(R / 65u);   /* 65-96 */
     /* > 96 rows: ceil(n / 128) <= n / 128 + 1 tiles each */
     caps[3] = (uint32_t)(R / 128u) + upto(R / 97u);
+}
+
+bool build_tiles_all(const MfmaBuffers &B, const uint32_t *counts, const uint32_t *offsets,
+                     const k3_moe_expert *experts, uint32_t E, hipStream_t st) {
+    if (E > 1024u) return false;
+    hipLaunchKernelGGL(tile_build_kernel, dim3(1), dim3(1024), 0, st, B, counts, offsets, experts,
+                       E, 1u);
+    return hipGetLastError() == hipSuccess;
 }
 
 bool mfma_supported(const k3_moe_shape &s) {

@@ -244,34 +244,55 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to
 /* ------------------------------------------------------------------------ */
 
 /*
- * grid (F / (4 * RW), E_upper), block 256. blockIdx.y indexes the selected
- * expert list; blocks beyond the selected count exit. Rows of the plan for
- * this expert are processed in tiles of TT tokens; the weight group loaded
- * for a tile is reused by all of its tokens.
+ * Work of a grouped exact workgroup: runs of plan rows [base, base + n) of
+ * an expert e. Tile mode (list == nullptr): the tiles of the per-class
+ * lists (at most 128 rows each, every selected expert; build_tiles_all),
+ * walked with stride gridDim.y, so a heavy expert's rows spread over many
+ * workgroups and no workgroup is launched past the tile count. List mode:
+ * list = (count, expert ids), walked the same way, each expert's rows
+ * whole (the MFMA path's fallback for experts whose tensors are not
+ * 16-byte aligned).
  */
-template <int RW, int TT>
-__global__ __launch_bounds__(256) void grouped_gateup_kernel(
-        uint16_t *__restrict__ act, const uint16_t *__restrict__ x,
-        const uint32_t *__restrict__ unique, const uint32_t *__restrict__ summary,
-        const uint32_t *__restrict__ counts, const uint32_t *__restrict__ offsets,
-        const uint32_t *__restrict__ token_index, const k3_moe_expert *__restrict__ experts,
-        uint32_t H, uint32_t F, uint32_t kind, float beta, float lb, const uint32_t *list) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
-    if (row0 >= F) return;
-    /* blockIdx.y indexes the selected experts, or with `list` (count, ids)
-     * walks that list with stride gridDim.y */
-    for (uint32_t q = blockIdx.y;; q += gridDim.y) {
-    uint32_t e;
-    if (list) {
-        if (q >= list[0]) return;
-        e = list[1u + q];
-    } else {
-        if (q != blockIdx.y || q >= summary[0]) return;
-        e = unique[q];
+struct ExactWork {
+    const uint32_t *tiles, *tile_count;
+    uint32_t cap[kTileClasses];
+    const uint32_t *list;       /* list mode: expert ids */
+    const uint32_t *list_count; /* their count */
+    const uint32_t *counts, *offsets;
+};
+
+/* Tile q of the tile lists (classes in order, tile_count[c] of class c
+ * stored from the class's segment start); false past the last. */
+__device__ __forceinline__ bool exact_tile(const ExactWork &W, uint32_t q, uint32_t &e,
+                                           uint32_t &base, uint32_t &n) {
+    uint32_t first = 0u;
+#pragma unroll
+    for (int c = 0; c < kTileClasses; c++) {
+        const uint32_t tc = W.tile_count[c];
+        if (q < tc) {
+            const uint32_t *t = W.tiles + 3u * (first + q);
+            e = t[0];
+            base = t[1];
+            n = t[2];
+            return true;
+        }
+        q -= tc;
+        first += W.cap[c];
     }
-    const uint32_t n = counts[e], base = offsets[e];
-    const k3_moe_expert ex = experts[e];
+    return false;
+}
+
+/* Gate/up of plan rows [base, base + n) of expert e, weight rows row0 ..
+ * row0 + RW of this wave: rows are processed TT tokens at a time, and the
+ * weight group loaded for them is reused by all TT. */
+template <int RW, int TT>
+__device__ __forceinline__ void gateup_rows(uint16_t *__restrict__ act,
+                                            const uint16_t *__restrict__ x,
+                                            const uint32_t *__restrict__ token_index,
+                                            const k3_moe_expert &ex, uint32_t base, uint32_t n,
+                                            uint32_t row0, uint32_t H, uint32_t F, uint32_t kind,
+                                            float beta, float lb) {
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t G = H / 32u;
     const uint8_t *gp = (const uint8_t *)ex.gate_packed + (uint64_t)row0 * (H / 2u);
     const uint8_t *up = (const uint8_t *)ex.up_packed + (uint64_t)row0 * (H / 2u);
@@ -320,31 +341,39 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
                     f32_to_bf16(gated_act(bf16_round(v), bf16_round(uu), kind, beta, lb));
         }
     }
+}
+
+/* grid (F / (4 * RW), walk), block 256 (ExactWork). */
+template <int RW, int TT>
+__global__ __launch_bounds__(256, 2) void grouped_gateup_kernel(
+        uint16_t *__restrict__ act, const uint16_t *__restrict__ x, ExactWork W,
+        const uint32_t *__restrict__ token_index, const k3_moe_expert *__restrict__ experts,
+        uint32_t H, uint32_t F, uint32_t kind, float beta, float lb) {
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
+    if (row0 >= F) return;
+    if (!W.list) {
+        uint32_t e, base, n;
+        for (uint32_t q = blockIdx.y; exact_tile(W, q, e, base, n); q += gridDim.y)
+            gateup_rows<RW, TT>(act, x, token_index, experts[e], base, n, row0, H, F, kind, beta,
+                                lb);
+        return;
+    }
+    for (uint32_t q = blockIdx.y; q < *W.list_count; q += gridDim.y) {
+        const uint32_t e = W.list[q];
+        gateup_rows<RW, TT>(act, x, token_index, experts[e], W.offsets[e], W.counts[e], row0, H,
+                            F, kind, beta, lb);
     }
 }
 
-/* grid (H / (4 * RB), E_upper), block 256: y[route] = down_e . act[row]. */
+/* Down of plan rows [base, base + n) of expert e into their route slots of
+ * y, weight rows row0 .. row0 + RB of this wave, TT tokens at a time. */
 template <int RB, int TT>
-__global__ __launch_bounds__(256) void grouped_down_kernel(
-        uint16_t *__restrict__ y, const uint16_t *__restrict__ act,
-        const uint32_t *__restrict__ unique, const uint32_t *__restrict__ summary,
-        const uint32_t *__restrict__ counts, const uint32_t *__restrict__ offsets,
-        const uint32_t *__restrict__ route_index, const k3_moe_expert *__restrict__ experts,
-        uint32_t H, uint32_t F, const uint32_t *list) {
+__device__ __forceinline__ void down_rows(uint16_t *__restrict__ y,
+                                          const uint16_t *__restrict__ act,
+                                          const uint32_t *__restrict__ route_index,
+                                          const k3_moe_expert &ex, uint32_t base, uint32_t n,
+                                          uint32_t row0, uint32_t H, uint32_t F) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RB;
-    if (row0 >= H) return;
-    for (uint32_t q = blockIdx.y;; q += gridDim.y) { /* as grouped_gateup_kernel */
-    uint32_t e;
-    if (list) {
-        if (q >= list[0]) return;
-        e = list[1u + q];
-    } else {
-        if (q != blockIdx.y || q >= summary[0]) return;
-        e = unique[q];
-    }
-    const uint32_t n = counts[e], base = offsets[e];
-    const k3_moe_expert ex = experts[e];
     const uint32_t G = F / 32u;
     const uint8_t *dp = (const uint8_t *)ex.down_packed + (uint64_t)row0 * (F / 2u);
     const bool a16 = ((uintptr_t)dp % 16u) == 0u;
@@ -383,6 +412,27 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
                 y[(uint64_t)route_index[base + p0 + t] * H + row0 + owner] = f32_to_bf16(v);
         }
     }
+}
+
+/* grid (H / (4 * RB), walk), block 256: y[route] = down_e . act[row]. Two
+ * waves per SIMD (at most 256 VGPRs): at one wave per SIMD (269 VGPRs) the
+ * kernel took 15.0 against 8.7 ms at cfg3. */
+template <int RB, int TT>
+__global__ __launch_bounds__(256, 2) void grouped_down_kernel(
+        uint16_t *__restrict__ y, const uint16_t *__restrict__ act, ExactWork W,
+        const uint32_t *__restrict__ route_index, const k3_moe_expert *__restrict__ experts,
+        uint32_t H, uint32_t F) {
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RB;
+    if (row0 >= H) return;
+    if (!W.list) {
+        uint32_t e, base, n;
+        for (uint32_t q = blockIdx.y; exact_tile(W, q, e, base, n); q += gridDim.y)
+            down_rows<RB, TT>(y, act, route_index, experts[e], base, n, row0, H, F);
+        return;
+    }
+    for (uint32_t q = blockIdx.y; q < *W.list_count; q += gridDim.y) {
+        const uint32_t e = W.list[q];
+        down_rows<RB, TT>(y, act, route_index, experts[e], W.offsets[e], W.counts[e], row0, H, F);
     }
 }
 
@@ -537,7 +587,11 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
                      ws.route_index, ws.chunk_base, ws.ids, T, k, E, st))
         return false;
     const uint32_t upper = (uint64_t)T * k < E ? T * k : E;
-    constexpr int RW = 4, TT = 4, RB = 4;
+    /* weight rows per wave and tokens per weight load: gate/up 2 x 2
+     * (255 VGPRs), down 4 x 4 (two waves per SIMD). Measured against 4 x 4
+     * / 2 x 2 / 2 x 1 / 1 x 2 shapes on cfg3 and cfg4: 26.5 and 387 ms per
+     * layer, the next best 29.2 and 419 ms. */
+    constexpr int RW = 2, TT = 2, RB = 4, TD = 4;
     if (precision != K3_MOE_EXACT) {
         if (!mfma_launch_experts(ws.mfma, ws.y, (const uint16_t *)hidden, ws.counts, ws.offsets,
                                  ws.token_index, ws.route_index, experts, s, T,
@@ -547,15 +601,17 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
          * the exact kernels, after the MFMA down kernel has consumed the
          * activation codes that share `act` */
         const uint32_t walk = upper < kFallbackExperts ? upper : kFallbackExperts;
+        ExactWork W{};
+        W.list_count = ws.mfma.unaligned;
+        W.list = ws.mfma.unaligned + 1;
+        W.counts = ws.counts;
+        W.offsets = ws.offsets;
         hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_gateup_kernel<RW, TT>),
                            dim3(F / (4u * RW), walk), dim3(256), 0, st, ws.act,
-                           (const uint16_t *)hidden, ws.unique, ws.summary, ws.counts, ws.offsets,
-                           ws.token_index, experts, H, F, s.activation, beta, lb,
-                           (const uint32_t *)ws.mfma.unaligned);
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TT>), dim3(H / (4u * RB), walk),
-                           dim3(256), 0, st, ws.y, ws.act, ws.unique, ws.summary, ws.counts,
-                           ws.offsets, ws.route_index, experts, H, F,
-                           (const uint32_t *)ws.mfma.unaligned);
+                           (const uint16_t *)hidden, W, ws.token_index, experts, H, F,
+                           s.activation, beta, lb);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TD>), dim3(H / (4u * RB), walk),
+                           dim3(256), 0, st, ws.y, ws.act, W, ws.route_index, experts, H, F);
         mark(K3_MOE_STAGE_COMBINE);
         hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
                            dim3(kCombineThreads), 0, st, (uint16_t *)output, ws.y,
@@ -564,14 +620,20 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
         return hipGetLastError() == hipSuccess;
     }
     mark(K3_MOE_STAGE_GATE_UP);
+    /* exact: workgroups over the tile lists of every selected expert */
+    if (!build_tiles_all(ws.mfma, ws.counts, ws.offsets, experts, E, st)) return false;
+    ExactWork W{};
+    W.tiles = ws.mfma.tiles;
+    W.tile_count = ws.mfma.tile_count;
+    for (int c = 0; c < kTileClasses; c++) W.cap[c] = ws.mfma.tile_cap[c];
+    W.counts = ws.counts;
+    W.offsets = ws.offsets;
     hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_gateup_kernel<RW, TT>), dim3(F / (4u * RW), upper),
-                       dim3(256), 0, st, ws.act, (const uint16_t *)hidden, ws.unique, ws.summary,
-                       ws.counts, ws.offsets, ws.token_index, experts, H, F, s.activation, beta,
-                       lb, nullptr);
+                       dim3(256), 0, st, ws.act, (const uint16_t *)hidden, W, ws.token_index,
+                       experts, H, F, s.activation, beta, lb);
     mark(K3_MOE_STAGE_DOWN);
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TT>), dim3(H / (4u * RB), upper),
-                       dim3(256), 0, st, ws.y, ws.act, ws.unique, ws.summary, ws.counts,
-                       ws.offsets, ws.route_index, experts, H, F, nullptr);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TD>), dim3(H / (4u * RB), upper),
+                       dim3(256), 0, st, ws.y, ws.act, W, ws.route_index, experts, H, F);
     mark(K3_MOE_STAGE_COMBINE);
     hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
                        dim3(kCombineThreads), 0, st, (uint16_t *)output, ws.y,
