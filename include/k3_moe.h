@@ -237,17 +237,28 @@ bool k3_moe_experts_bf16(void *output, const void *hidden, const void *residual,
 
 /*
  * MXFP8 quantisation of `count` bf16 values (count % 32 == 0; src and the
- * code arrays 16-byte aligned) as the MFMA precisions feed activations:
- * per block of 32, X = floor(log2(max |x|)) - 8 (+1 if the maximum would
- * exceed 448 after scaling; >= -127), scale byte X + 127, codes E4M3(x *
- * 2^-X) rounded to nearest even. With lo_codes/lo_scales non-NULL the
- * residual x - hi is quantised the same way (the two-term split of
- * K3_MOE_MFMA). No reference counterpart: exported so callers and tests
- * can check the activation encoding on its own.
+ * code arrays 16-byte aligned) as the MFMA precisions feed the gate/up
+ * activation to the down products: per block of 32, X = floor(log2(max
+ * |x|)) - 8 (+1 if the maximum would exceed 448 after scaling; >= -127),
+ * scale byte X + 127, codes E4M3(x * 2^-X) rounded to nearest even. With
+ * lo_codes/lo_scales non-NULL the residual x - hi is quantised the same
+ * way (the two-term split of K3_MOE_MFMA). No reference counterpart:
+ * exported so callers and tests can check the activation encoding on its
+ * own.
  */
 bool k3_moe_mx8_quantize_bf16(uint8_t *hi_codes, uint8_t *hi_scales, uint8_t *lo_codes,
                               uint8_t *lo_scales, const void *src, uint64_t count,
                               void *stream);
+
+/*
+ * The same encoding with one scale per row (and term) of a [rows, cols]
+ * bf16 matrix (cols % 8 == 0; src 16-byte and the code arrays 8-byte
+ * aligned; scale arrays of `rows` bytes): how the MFMA precisions feed the
+ * token rows to the gate/up products. No reference counterpart.
+ */
+bool k3_moe_mx8_quantize_rows_bf16(uint8_t *hi_codes, uint8_t *hi_scales, uint8_t *lo_codes,
+                                   uint8_t *lo_scales, const void *src, uint32_t rows,
+                                   uint32_t cols, void *stream);
 
 /*
  * K3-native MoE layer: the routed experts run on a latent of width D (the

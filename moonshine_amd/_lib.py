@@ -126,6 +126,7 @@ SIGNATURES = {
     "k3_moe_synth_fill": (_b, [_p, _u64, _u64, _u64, _u32, _p]),
     "k3_moe_synth_fill_host": (None, [_p, _u64, _u64, _u64, _u32]),
     "k3_moe_mx8_quantize_bf16": (_b, [_p, _p, _p, _p, _p, _u64, _p]),
+    "k3_moe_mx8_quantize_rows_bf16": (_b, [_p, _p, _p, _p, _p, _u32, _u32, _p]),
 }
 
 _lib = None

@@ -1,14 +1,15 @@
 /*
  * Grouped expert products on CDNA4 scaled MFMA (prefill / batched tokens).
  *
- * Activations enter the MFMA as MXFP8 (E4M3 codes, one E8M0 scale per 32
- * along K) against the experts' native MXFP4 weights, through
- * V_MFMA_SCALE_F32_16X16X128_F8F6F4. In the split precision every bf16
- * activation is carried as two MXFP8 terms hi + lo (lo quantizes x - hi),
- * which reproduces it exactly except for elements more than 2^6 below their
- * block maximum (error <= 2^-22 of that maximum), so the products are those
- * of the bf16 inputs and only the fp32 accumulation order differs from the
- * exact path.
+ * Activations enter the MFMA as E4M3 codes with E8M0 scales against the
+ * experts' native MXFP4 weights, through V_MFMA_SCALE_F32_16X16X128_F8F6F4:
+ * the token rows x with one scale per row (and term), the gate/up
+ * activation with one per 32 columns (MXFP8). In the split precision every
+ * bf16 value is carried as two terms hi + lo (lo quantizes x - hi), which
+ * reproduces it exactly except for elements more than 2^6 below the
+ * maximum of their scale run (error <= 2^-22 of that maximum), so the
+ * products are those of the bf16 inputs and only the fp32 accumulation
+ * order differs from the exact path.
  */
 #pragma once
 
@@ -26,8 +27,10 @@ namespace k3 {
 constexpr int kTileClasses = 4;
 
 struct MfmaBuffers {
-    uint8_t *xq[2], *xs[2];     /* [T, H] codes, [T, H / 32] scales: hi, lo */
-    uint8_t *aq[2], *as[2];     /* [routes, F] codes, [routes, F / 32] scales */
+    uint8_t *xq[2], *xs[2];     /* [T, H] codes, [T] row scales: hi, lo */
+    uint8_t *aq[2], *as[2];     /* [routes, F] codes; scales [F / 512][routes][16]
+                                   (16 scale bytes = 512 columns of a row) */
+    uint32_t routes;            /* rows of aq / as */
     uint32_t *tiles;            /* kTileClasses x tile_cap x {expert, row0, rows} */
     uint32_t *tile_count;       /* [kTileClasses] */
     uint32_t *unaligned;        /* [E + 1]: count, then the selected experts with a

@@ -81,6 +81,98 @@ __global__ __launch_bounds__(256) void x_split_kernel(MfmaBuffers B, const uint1
     }
 }
 
+/* Maximum over the 256 threads of a block (values >= 0; NaN ignored). */
+__device__ __forceinline__ float block_max256(float m, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    __syncthreads(); /* red is reused by consecutive calls */
+    if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+/* Codes of 8 values under one scale (inverse inv), and their residuals
+ * v - code x sc in v (exact products, one rounding). */
+template <bool Residual>
+__device__ __forceinline__ uint2 e4m3x8(float (&v)[8], float inv, float sc) {
+    uint32_t w[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float *u = v + 4 * h;
+        uint32_t word = e4m3x2<false>(__fmul_rn(u[0], inv), __fmul_rn(u[1], inv), 0u);
+        word = e4m3x2<true>(__fmul_rn(u[2], inv), __fmul_rn(u[3], inv), word);
+        if constexpr (Residual) {
+            u[0] = __fsub_rn(u[0], __fmul_rn(e4m3_byte<0>(word), sc));
+            u[1] = __fsub_rn(u[1], __fmul_rn(e4m3_byte<1>(word), sc));
+            u[2] = __fsub_rn(u[2], __fmul_rn(e4m3_byte<2>(word), sc));
+            u[3] = __fsub_rn(u[3], __fmul_rn(e4m3_byte<3>(word), sc));
+        }
+        w[h] = word;
+    }
+    return make_uint2(w[0], w[1]);
+}
+
+__device__ __forceinline__ void bf16x8_to_f32(uint4 p, float (&v)[8]) {
+    const uint32_t d[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = bf16_lo(d[i]);
+        v[2 * i + 1] = bf16_hi(d[i]);
+    }
+}
+
+/*
+ * One block of 256 threads per token row of [T, H] bf16 (H % 8 == 0): the
+ * row's E4M3 codes under one E8M0 scale per term (the scale rule of the
+ * 32-element MXFP8 blocks applied to the whole row), hi and, for two
+ * terms, lo = x - hi under its own scale. The row is read once per pass
+ * (maximum, residual maximum, codes); after the first it comes from L2.
+ * With one scale per row the MFMA lanes hold their rows' scales in
+ * registers for the whole K loop instead of staging scale bytes per step.
+ */
+template <int TERMS>
+__global__ __launch_bounds__(256) void x_split_rows_kernel(MfmaBuffers B,
+                                                           const uint16_t *__restrict__ x,
+                                                           uint32_t H) {
+    __shared__ float red[4];
+    const uint32_t row = blockIdx.x, chunks = H / 8u;
+    const uint4 *src = (const uint4 *)(x + (uint64_t)row * H);
+    float amax = 0.0f;
+    for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
+        float v[8];
+        bf16x8_to_f32(src[q], v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+    }
+    const uint32_t s0 = mx8_scale_byte(block_max256(amax, red));
+    const float inv0 = mx8_inv_scale(s0), sc0 = e8m0_to_f32(s0);
+    uint32_t s1 = 0u;
+    if constexpr (TERMS == 2) {
+        float rmax = 0.0f;
+        for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
+            float v[8];
+            bf16x8_to_f32(src[q], v);
+            (void)e4m3x8<true>(v, inv0, sc0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) rmax = fmaxf(rmax, fabsf(v[i]));
+        }
+        s1 = mx8_scale_byte(block_max256(rmax, red));
+    }
+    const float inv1 = mx8_inv_scale(s1);
+    uint2 *hq = (uint2 *)(B.xq[0] + (uint64_t)row * H);
+    uint2 *lq = (uint2 *)(B.xq[TERMS - 1] + (uint64_t)row * H);
+    for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
+        float v[8];
+        bf16x8_to_f32(src[q], v);
+        hq[q] = e4m3x8<TERMS == 2>(v, inv0, sc0);
+        if constexpr (TERMS == 2) lq[q] = e4m3x8<false>(v, inv1, 0.0f);
+    }
+    if (threadIdx.x == 0u) {
+        B.xs[0][row] = (uint8_t)s0;
+        if constexpr (TERMS == 2) B.xs[1][row] = (uint8_t)s1;
+    }
+}
+
 /* ---------------------------------------------------------------------- */
 /* tile lists                                                              */
 /* ---------------------------------------------------------------------- */
@@ -241,8 +333,21 @@ struct TileCfg {
     static constexpr int loads(int mask) {
         return ((mask & 8) ? DA::per : 0) + ((mask & 4) ? DB::per : 0);
     }
+    /* activation scales: per row in registers (RowScaled) or staged */
+    static constexpr bool AROW = false;
     static_assert(LDS <= 160 * 1024, "LDS");
     static_assert(loads(15) < 32, "vmcnt budget for one step in flight");
+};
+
+/* A tile class for the gate/up kernel: the token rows carry one scale per
+ * row and term (x_split_rows_kernel), held in registers, so no activation
+ * scale chunks are staged or read per step. */
+template <class C>
+struct RowScaled : C {
+    static constexpr bool AROW = true;
+    static constexpr int SA_CH = 0, OFF_SA = 0, OFF_SB = 0, SBUF = C::SB_CH * 1024;
+    static constexpr int LDS = C::STAGE * C::STAGES + 2 * SBUF;
+    using DSA = Deal<0, C::NWV>;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -270,7 +375,8 @@ struct Loader {
     const uint8_t *b[C::DB::per > 0 ? C::DB::per : 1];
     const uint8_t *sa[C::DSA::per > 0 ? C::DSA::per : 1];
     const uint8_t *sb[C::DSB::per > 0 ? C::DSB::per : 1];
-    uint32_t mask; /* kinds held: bit 3 A, 2 B, 1 SA, 0 SB */
+    uint32_t mask;      /* kinds held: bit 3 A, 2 B, 1 SA, 0 SB */
+    uint32_t sa_stride; /* bytes between consecutive scale blocks of an SA row */
 };
 
 /* chunk index of slot q of a kind for this wave */
@@ -296,7 +402,7 @@ __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, u
         if (L.mask & 2u) {
 #pragma unroll
             for (int q = 0; q < C::DSA::per; q++)
-                dma<16>(L.sa[q] + 16u * b, sbuf + C::OFF_SA + 1024 * chunk_of<typename C::DSA, W>(q, wave));
+                dma<16>(L.sa[q] + L.sa_stride * b, sbuf + C::OFF_SA + 1024 * chunk_of<typename C::DSA, W>(q, wave));
         }
         if (L.mask & 1u) {
 #pragma unroll
@@ -383,12 +489,21 @@ __device__ __forceinline__ void wait_lgkm() {
  * soon as its reads have landed (lgkmcnt(count of the second half's
  * reads)), so the second half's LDS reads run under them.
  */
+/* Activation scale bytes of a wave's rows when they are per row (C::AROW):
+ * v[t][i] for term t, row block i (lane row c). */
+template <class C>
+struct RowScales {
+    uint32_t v[C::TERMS][C::WM];
+};
+
 template <class C, int KSI>
 __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
                                            const uint8_t *sbuf, uint32_t sq, uint32_t wm,
-                                           uint32_t wn, uint32_t live) {
+                                           uint32_t wn, uint32_t live, const RowScales<C> &rs) {
     constexpr int NA = C::TERMS * C::WM, H1 = (NA + 1) / 2, H2 = NA - H1;
-    static_assert(3 * H2 < 16, "second-half reads fit the lgkm counter");
+    /* LDS reads per A fragment: two code halves (+ its scale dword) */
+    constexpr int RA = C::AROW ? 2 : 3;
+    static_assert(RA * H2 < 16, "second-half reads fit the lgkm counter");
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t base = lds_addr(st);
@@ -410,13 +525,17 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         constexpr int off = C::OFF_A + 2048 * ((KSI * C::TERMS + t) * (C::BM / 16) + i);
         alo[q] = ds_read16<off>(a_lo);
         ahi[q] = ds_read16<off>(a_hi);
-        saw[q] = ds_read4<16 * (t * C::SA_ROWS + 16 * i)>(sa_base);
+        if constexpr (!C::AROW) saw[q] = ds_read4<16 * (t * C::SA_ROWS + 16 * i)>(sa_base);
     };
     auto mfmas = [&](auto Q) {
         constexpr int q = decltype(Q)::value, i = q % C::WM;
         const i32x8 af = i32x8{(int)alo[q].x, (int)alo[q].y, (int)alo[q].z, (int)alo[q].w,
                                (int)ahi[q].x, (int)ahi[q].y, (int)ahi[q].z, (int)ahi[q].w};
-        const int sa = (int)((saw[q] >> (8u * g)) & 255u);
+        int sa;
+        if constexpr (C::AROW)
+            sa = (int)rs.v[q / C::WM][i];
+        else
+            sa = (int)((saw[q] >> (8u * g)) & 255u);
         if ((uint32_t)i >= live) return; /* row block past the tile's rows */
         static_for<C::WN>([&](auto J) {
             constexpr int j = decltype(J)::value;
@@ -443,7 +562,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
             constexpr int q = decltype(Q)::value;
             if constexpr (q + 1 < NA) {
                 read_a(std::integral_constant<int, q + 1>{});
-                wait_lgkm<3>();
+                wait_lgkm<RA>();
             } else {
                 wait_lgkm<0>();
             }
@@ -455,7 +574,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
             }
             after_wait(alo[q]);
             after_wait(ahi[q]);
-            after_wait(saw[q]);
+            if constexpr (!C::AROW) after_wait(saw[q]);
             mfmas(Q);
             __builtin_amdgcn_sched_barrier(0);
         });
@@ -474,7 +593,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         static_for<H1>([&](auto I) {
             after_wait(alo[decltype(I)::value]);
             after_wait(ahi[decltype(I)::value]);
-            after_wait(saw[decltype(I)::value]);
+            if constexpr (!C::AROW) after_wait(saw[decltype(I)::value]);
         });
         static_for<H1>([&](auto I) { mfmas(I); });
         __builtin_amdgcn_sched_barrier(0);
@@ -484,7 +603,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
             constexpr int q = H1 + decltype(I)::value;
             after_wait(alo[q]);
             after_wait(ahi[q]);
-            after_wait(saw[q]);
+            if constexpr (!C::AROW) after_wait(saw[q]);
         });
         static_for<H2>([&](auto I) { mfmas(std::integral_constant<int, H1 + decltype(I)::value>{}); });
         return;
@@ -492,7 +611,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
     static_for<H1>([&](auto I) { read_a(I); });
     static_for<H2>([&](auto I) { read_a(std::integral_constant<int, H1 + decltype(I)::value>{}); });
     /* first half (and B) landed */
-    wait_lgkm<3 * H2>();
+    wait_lgkm<RA * H2>();
     static_for<C::WN>([&](auto J) {
         after_wait(bv[decltype(J)::value]);
         after_wait(sbw[decltype(J)::value]);
@@ -500,7 +619,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
     static_for<H1>([&](auto I) {
         after_wait(alo[decltype(I)::value]);
         after_wait(ahi[decltype(I)::value]);
-        after_wait(saw[decltype(I)::value]);
+        if constexpr (!C::AROW) after_wait(saw[decltype(I)::value]);
     });
     static_for<H1>([&](auto I) { mfmas(I); });
     __builtin_amdgcn_sched_barrier(0);
@@ -509,7 +628,7 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         constexpr int q = H1 + decltype(I)::value;
         after_wait(alo[q]);
         after_wait(ahi[q]);
-        after_wait(saw[q]);
+        if constexpr (!C::AROW) after_wait(saw[q]);
     });
     static_for<H2>([&](auto I) { mfmas(std::integral_constant<int, H1 + decltype(I)::value>{}); });
 }
@@ -518,13 +637,14 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
 template <class C>
 __device__ __forceinline__ void mfma_step(f32x4 (&acc)[C::WM][C::WN], const uint8_t *st,
                                           const uint8_t *sbuf0, const uint8_t *sbuf1, uint32_t s,
-                                          uint32_t wm, uint32_t wn, uint32_t live) {
+                                          uint32_t wm, uint32_t wn, uint32_t live,
+                                          const RowScales<C> &rs) {
     const uint32_t b = s / (uint32_t)C::SQ, sq = s % (uint32_t)C::SQ;
     const uint8_t *sbuf = (b & 1u) ? sbuf1 : sbuf0;
-    mfma_slice<C, 0>(acc, st, sbuf, sq, wm, wn, live);
+    mfma_slice<C, 0>(acc, st, sbuf, sq, wm, wn, live, rs);
     if constexpr (C::KS == 2) {
         __builtin_amdgcn_sched_barrier(0);
-        mfma_slice<C, 1>(acc, st, sbuf, sq, wm, wn, live);
+        mfma_slice<C, 1>(acc, st, sbuf, sq, wm, wn, live, rs);
     }
 }
 
@@ -536,11 +656,12 @@ template <class C>
 __device__ __forceinline__ void ring_step(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
                                           const uint8_t *cur, uint8_t *nxt, uint32_t s,
                                           uint32_t nsteps, uint32_t wm, uint32_t wn,
-                                          uint8_t *sbuf0, uint8_t *sbuf1, uint32_t live) {
+                                          uint8_t *sbuf0, uint8_t *sbuf1, uint32_t live,
+                                          const RowScales<C> &rs) {
     wait_step<C>(L, s + 1u < nsteps ? 1 : 0);
     __builtin_amdgcn_s_barrier();
     if (s + 2u < nsteps) issue_step<C>(L, nxt, s + 2u, threadIdx.x >> 6, sbuf0, sbuf1);
-    mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn, live);
+    mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn, live, rs);
 }
 
 /* 16-row blocks of wave row wm that hold tile rows (< rows): MFMAs of
@@ -564,7 +685,7 @@ template <class C>
 __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const Loader<C> &L,
                                               uint8_t *b0, uint8_t *b1, uint8_t *b2, uint8_t *sbuf0,
                                               uint8_t *sbuf1, uint32_t K, uint32_t wm,
-                                              uint32_t wn, uint32_t live) {
+                                              uint32_t wn, uint32_t live, const RowScales<C> &rs) {
     static_assert(C::STAGES == 2 || C::STAGES == 3, "two or three buffers");
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t nsteps = K / (uint32_t)C::KSTEP;
@@ -576,7 +697,7 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
             wait_vm<0>();
             __builtin_amdgcn_s_barrier();
             if (s + 1u < nsteps) issue_step<C>(L, nxt, s + 1u, wave, sbuf0, sbuf1);
-            mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn, live);
+            mfma_step<C>(acc, cur, sbuf0, sbuf1, s, wm, wn, live, rs);
         };
         issue_step<C>(L, b0, 0u, wave, sbuf0, sbuf1);
         for (uint32_t s = 0; s < nsteps; s += 2u) {
@@ -588,9 +709,11 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
     issue_step<C>(L, b0, 0u, wave, sbuf0, sbuf1);
     if (nsteps > 1u) issue_step<C>(L, b1, 1u, wave, sbuf0, sbuf1);
     for (uint32_t s = 0; s < nsteps; s += 3u) {
-        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn, sbuf0, sbuf1, live);
-        if (s + 1u < nsteps) ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn, sbuf0, sbuf1, live);
-        if (s + 2u < nsteps) ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn, sbuf0, sbuf1, live);
+        ring_step<C>(acc, L, b0, b2, s, nsteps, wm, wn, sbuf0, sbuf1, live, rs);
+        if (s + 1u < nsteps)
+            ring_step<C>(acc, L, b1, b0, s + 1u, nsteps, wm, wn, sbuf0, sbuf1, live, rs);
+        if (s + 2u < nsteps)
+            ring_step<C>(acc, L, b2, b1, s + 2u, nsteps, wm, wn, sbuf0, sbuf1, live, rs);
     }
 }
 
@@ -722,8 +845,11 @@ __device__ __forceinline__ void gateup_epilogue(const f32x4 (&acc)[C::WM][C::WN]
                     *(uint32_t *)dst = w;
                 else
                     *(uint16_t *)dst = (uint16_t)w;
-                if (c % (uint32_t)LB == 0u)
-                    A.B.as[t][prow * (F / 32u) + fw0 / 32u + c / (uint32_t)LB] = (uint8_t)sbyte;
+                if (c % (uint32_t)LB == 0u) { /* block-major: [kb / 16][route][kb % 16] */
+                    const uint32_t kb = fw0 / 32u + c / (uint32_t)LB;
+                    A.B.as[t][(((uint64_t)(kb >> 4) * A.B.routes + prow) << 4) + (kb & 15u)] =
+                        (uint8_t)sbyte;
+                }
             }
         }
         /* one row at a time: interleaving rows raises the register
@@ -772,9 +898,6 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     auto a_row = [&](int t, uint32_t r) -> const uint8_t * {
         return A.B.xq[t] + (uint64_t)tok(r) * H;
     };
-    auto a_scl = [&](int t, uint32_t r) -> const uint8_t * {
-        return A.B.xs[t] + (uint64_t)tok(r) * (H / 32u);
-    };
     Loader<C> L;
     {
         const uint8_t *gp = (const uint8_t *)ex.gate_packed, *up = (const uint8_t *)ex.up_packed;
@@ -811,20 +934,22 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
             const int ch = min(chunk_of<typename C::DSB, W>(q, wave), C::SB_CH - 1);
             L.sb[q] = wr_scl(ch * 4 + (int)g, c);
         }
+        static_assert(C::AROW, "gate/up takes per-row activation scales");
+        L.sa_stride = 0u;
+    }
+    RowScales<C> rs; /* lane row c of each of the wave's row blocks */
 #pragma unroll
-        for (int q = 0; q < C::DSA::per; q++) {
-            const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
-            const int t = ch / (C::SA_ROWS / 64);
-            const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
-            L.sa[q] = a_scl(t, r);
-        }
+    for (int i = 0; i < C::WM; i++) {
+        const uint32_t tk = tok(16u * (wm * (uint32_t)C::WM + (uint32_t)i) + c);
+#pragma unroll
+        for (int t = 0; t < C::TERMS; t++) rs.v[t][i] = A.B.xs[t][tk];
     }
     f32x4 acc[C::WM][C::WN];
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, H, wm, wn, live_blocks<C>(rows, wm));
+    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, H, wm, wn, live_blocks<C>(rows, wm), rs);
 
     const uint32_t fw0 = f0 + (uint32_t)FW * wn;
     gateup_epilogue<C, KIND>(acc, A, row0, rows, fw0, wm, g, c);
@@ -900,14 +1025,17 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
         const int ch = min(chunk_of<typename C::DSA, W>(q, wave), C::SA_CH - 1);
         const int t = ch / (C::SA_ROWS / 64);
         const uint32_t r = (uint32_t)((ch % (C::SA_ROWS / 64)) * 64) + lane;
-        L.sa[q] = A.B.as[t] + prow(r) * (F / 32u);
+        L.sa[q] = A.B.as[t] + prow(r) * 16u;
     }
+    L.sa_stride = 16u * A.B.routes; /* scale block b of every row at + b 16 routes */
     f32x4 acc[C::WM][C::WN];
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
         for (int j = 0; j < C::WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, F, wm, wn, live_blocks<C>(rows, wm));
+    static_assert(!C::AROW, "down stages the activation's block scales");
+    const RowScales<C> rs{};
+    mfma_pipeline<C>(acc, L, b0, b1, b2, sbuf0, sbuf1, F, wm, wn, live_blocks<C>(rows, wm), rs);
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
 #pragma unroll
@@ -943,8 +1071,11 @@ using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2, 2>;
 /* 128 x 512 blocks: eight waves, two per SIMD, each 64 activation rows x
  * 128 weight rows; halves the activation re-reads of a 256-wide block, two
  * stage buffers */
+#ifndef K3_C3
+#define K3_C3 2, 4, 4, 8, TERMS, 2
+#endif
 template <int TERMS>
-using Cls3 = TileCfg<2, 4, 4, 8, TERMS, 2>;
+using Cls3 = TileCfg<K3_C3>;
 /* 96 x 512 blocks for experts of 65-96 rows, one tile each (most experts
  * of a Zipf batch's 128-row range): a quarter less activation staging per
  * K step than a padded 128-row tile, 48 rows per wave. One term stages
@@ -954,7 +1085,10 @@ using Cls3 = TileCfg<2, 4, 4, 8, TERMS, 2>;
 #define K3_C2_AUX 0
 #endif
 template <int TERMS>
-using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, K3_C2_AUX>, Cls3<TERMS>>;
+#ifndef K3_C2
+#define K3_C2 2, 4, 3, 8, 2, 2, 1, K3_C2_AUX
+#endif
+using Cls2 = std::conditional_t<TERMS == 2, TileCfg<K3_C2>, Cls3<TERMS>>;
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
@@ -979,9 +1113,8 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
                   const uint32_t *route_index, const k3_moe_expert *experts, const k3_moe_shape &s,
                   uint32_t T, hipStream_t st, const StageMarker &mark) {
     const uint32_t H = s.hidden, F = s.ffn;
-    const uint64_t blocks = (uint64_t)T * H / 32u;
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_kernel<TERMS>), dim3((uint32_t)((blocks + 255u) / 256u)),
-                       dim3(256), 0, st, B, hidden, blocks);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<TERMS>), dim3(T), dim3(256), 0, st, B,
+                       hidden, H);
     hipLaunchKernelGGL(tile_build_kernel, dim3(1), dim3(1024), 0, st, B, counts, offsets,
                        experts, s.expert_count, 0u);
     mark(K3_MOE_STAGE_GATE_UP);
@@ -998,10 +1131,10 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         if (!B.tile_cap[c]) continue;
         ga.tiles = tl[c];
         ga.tile_count = B.tile_count + c;
-        if (c == 0) launch_gateup<Cls0G<TERMS>>(ga, B.tile_cap[c], st);
-        if (c == 1) launch_gateup<Cls1<TERMS>>(ga, B.tile_cap[c], st);
-        if (c == 2) launch_gateup<Cls2<TERMS>>(ga, B.tile_cap[c], st);
-        if (c == 3) launch_gateup<Cls3<TERMS>>(ga, B.tile_cap[c], st);
+        if (c == 0) launch_gateup<RowScaled<Cls0G<TERMS>>>(ga, B.tile_cap[c], st);
+        if (c == 1) launch_gateup<RowScaled<Cls1<TERMS>>>(ga, B.tile_cap[c], st);
+        if (c == 2) launch_gateup<RowScaled<Cls2<TERMS>>>(ga, B.tile_cap[c], st);
+        if (c == 3) launch_gateup<RowScaled<Cls3<TERMS>>>(ga, B.tile_cap[c], st);
     }
     mark(K3_MOE_STAGE_DOWN);
     for (int c = 0; c < kTileClasses; c++) {
@@ -1077,5 +1210,27 @@ extern "C" bool k3_moe_mx8_quantize_bf16(uint8_t *hi_codes, uint8_t *hi_scales, 
     else
         hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_kernel<1>), grid, dim3(256), 0,
                            (hipStream_t)stream, B, (const uint16_t *)src, blocks);
+    return hipGetLastError() == hipSuccess;
+}
+
+extern "C" bool k3_moe_mx8_quantize_rows_bf16(uint8_t *hi_codes, uint8_t *hi_scales,
+                                              uint8_t *lo_codes, uint8_t *lo_scales,
+                                              const void *src, uint32_t rows, uint32_t cols,
+                                              void *stream) {
+    using namespace k3;
+    if (!hi_codes || !hi_scales || !src || rows == 0u || cols == 0u || cols % 8u != 0u ||
+        ((uintptr_t)src % 16u) != 0u || ((uintptr_t)hi_codes % 8u) != 0u ||
+        ((lo_codes == nullptr) != (lo_scales == nullptr)) ||
+        (lo_codes && ((uintptr_t)lo_codes % 8u) != 0u))
+        return false;
+    MfmaBuffers B{};
+    B.xq[0] = hi_codes; B.xs[0] = hi_scales;
+    B.xq[1] = lo_codes; B.xs[1] = lo_scales;
+    if (lo_codes)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<2>), dim3(rows), dim3(256), 0,
+                           (hipStream_t)stream, B, (const uint16_t *)src, cols);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<1>), dim3(rows), dim3(256), 0,
+                           (hipStream_t)stream, B, (const uint16_t *)src, cols);
     return hipGetLastError() == hipSuccess;
 }

@@ -101,10 +101,11 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
         MfmaBuffers &m = w.mfma;
         for (int t = 0; t < 2; t++) {
             m.xq[t] = take(1ull * T * s.hidden);
-            m.xs[t] = take(1ull * T * s.hidden / 32u);
+            m.xs[t] = take(1ull * T);
             m.aq[t] = w.act ? (uint8_t *)w.act + (uint64_t)t * routes * s.ffn : nullptr;
             m.as[t] = take(1ull * routes * s.ffn / 32u);
         }
+        m.routes = (uint32_t)routes;
         mfma_tile_caps(T, s.top_k, s.expert_count, m.tile_cap);
         uint64_t ntiles = 0u;
         for (int c = 0; c < kTileClasses; c++) ntiles += m.tile_cap[c];

@@ -435,14 +435,15 @@ static int ilog2f_pos(float a) {
     return (31 - __builtin_clz(u & 0x7fffffu)) - 149;
 }
 
-/* MXFP8 quantization of one block of 32 fp32 values: X = floor(log2(max
- * |v|)) - 8, plus one when max |v| * 2^-X exceeds 448 (E4M3's largest
- * finite value, so nothing saturates), clamped to >= -127 (X = -127 for an
- * all-zero block); scale byte = X + 127, q = E4M3(v * 2^-X) rounded to
- * nearest even. The scaled maximum lands in (224, 448]. */
-static void mx8_block(uint8_t *q, uint8_t *scale, const float *v) {
+/* MXFP8 quantization of a run of n fp32 values sharing one scale (a block
+ * of 32, or a whole row): X = floor(log2(max |v|)) - 8, plus one when
+ * max |v| * 2^-X exceeds 448 (E4M3's largest finite value, so nothing
+ * saturates), clamped to >= -127 (X = -127 for an all-zero run); scale
+ * byte = X + 127, q = E4M3(v * 2^-X) rounded to nearest even. The scaled
+ * maximum lands in (224, 448]. */
+static void mx8_run(uint8_t *q, uint8_t *scale, const float *v, uint64_t n) {
     float amax = 0.0f;
-    for (int i = 0; i < 32; i++) {
+    for (uint64_t i = 0; i < n; i++) {
         const float a = fabsf(v[i]);
         amax = a > amax ? a : amax;
     }
@@ -454,7 +455,7 @@ static void mx8_block(uint8_t *q, uint8_t *scale, const float *v) {
     }
     *scale = (uint8_t)(X + 127);
     const float inv = X == -127 ? u2f(0x7f000000u) : u2f((uint32_t)(127 - X) << 23);
-    for (int i = 0; i < 32; i++) q[i] = k3o_f32_to_e4m3(v[i] * inv);
+    for (uint64_t i = 0; i < n; i++) q[i] = k3o_f32_to_e4m3(v[i] * inv);
 }
 
 static float mx8_value(uint8_t q, uint8_t scale) {
@@ -465,34 +466,61 @@ void k3o_mx8_quantize(uint8_t *q, uint8_t *scales, const uint16_t *src, uint64_t
     float v[32];
     for (uint64_t b = 0; b < n / 32u; b++) {
         for (int i = 0; i < 32; i++) v[i] = k3o_bf16_to_f32(src[32u * b + i]);
-        mx8_block(q + 32u * b, scales + b, v);
+        mx8_run(q + 32u * b, scales + b, v, 32u);
     }
 }
 
-/* Two-term MXFP8 split: hi = MXFP8(x), lo = MXFP8(x - hi) with its own
- * block scale (the difference is exact in fp32). hi + lo reproduces every
- * bf16 element whose exponent is within 2^-6 of its block maximum exactly,
- * and smaller ones to within 2^-22 of the block maximum. */
+/* Two-term MXFP8 split of a run of n values with one scale per term: hi =
+ * MXFP8(x), lo = MXFP8(x - hi) with its own scale (the difference is exact
+ * in fp32). hi + lo reproduces every bf16 element within 2^6 of the run's
+ * maximum exactly, and smaller ones to within 2^-22 of that maximum. v and
+ * r are scratch of n floats. */
+static void mx8_split_run(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
+                          const uint16_t *src, uint64_t n, float *v, float *r) {
+    for (uint64_t i = 0; i < n; i++) v[i] = k3o_bf16_to_f32(src[i]);
+    mx8_run(hi_q, hi_s, v, n);
+    for (uint64_t i = 0; i < n; i++) r[i] = v[i] - mx8_value(hi_q[i], *hi_s);
+    mx8_run(lo_q, lo_s, r, n);
+}
+
+/* Per 32-element block. */
 void k3o_mx8_split(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
                    const uint16_t *src, uint64_t n) {
     float v[32], r[32];
-    for (uint64_t b = 0; b < n / 32u; b++) {
-        for (int i = 0; i < 32; i++) v[i] = k3o_bf16_to_f32(src[32u * b + i]);
-        mx8_block(hi_q + 32u * b, hi_s + b, v);
-        for (int i = 0; i < 32; i++) r[i] = v[i] - mx8_value(hi_q[32u * b + i], hi_s[b]);
-        mx8_block(lo_q + 32u * b, lo_s + b, r);
+    for (uint64_t b = 0; b < n / 32u; b++)
+        mx8_split_run(hi_q + 32u * b, hi_s + b, lo_q + 32u * b, lo_s + b, src + 32u * b, 32u, v, r);
+}
+
+/* One scale per row (and term) of a [rows, cols] matrix: the encoding of
+ * the MFMA path's token rows, whose per-row scales stay in registers. */
+void k3o_mx8_quantize_rows(uint8_t *q, uint8_t *scales, const uint16_t *src, uint64_t rows,
+                           uint64_t cols) {
+    float *v = (float *)malloc(4u * cols);
+    for (uint64_t t = 0; t < rows; t++) {
+        for (uint64_t i = 0; i < cols; i++) v[i] = k3o_bf16_to_f32(src[t * cols + i]);
+        mx8_run(q + t * cols, scales + t, v, cols);
     }
+    free(v);
+}
+
+void k3o_mx8_split_rows(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
+                        const uint16_t *src, uint64_t rows, uint64_t cols) {
+    float *v = (float *)malloc(8u * cols);
+    for (uint64_t t = 0; t < rows; t++)
+        mx8_split_run(hi_q + t * cols, hi_s + t, lo_q + t * cols, lo_s + t, src + t * cols, cols,
+                      v, v + cols);
+    free(v);
 }
 
 /* bf16 bits of the split's reconstruction hi + lo, rounded to bf16 (it is
  * exactly x for every element that matters; used only to feed fp64). */
 static double mx_row_split(const uint8_t *p, const uint8_t *s, const uint8_t *hq,
                            const uint8_t *hs, const uint8_t *lq, const uint8_t *ls,
-                           uint32_t cols) {
+                           uint32_t cols, uint32_t sblk) {
     double acc = 0.0;
     for (uint32_t c = 0; c < cols; c++) {
-        const double xv = (double)mx8_value(hq[c], hs[c / 32u]) +
-                          (double)mx8_value(lq[c], ls[c / 32u]);
+        const double xv = (double)mx8_value(hq[c], hs[c / sblk]) +
+                          (double)mx8_value(lq[c], ls[c / sblk]);
         acc += (double)nib(p, c) * (double)k3o_e8m0(s[c / 32u]) * xv;
     }
     return acc;
@@ -500,11 +528,11 @@ static double mx_row_split(const uint8_t *p, const uint8_t *s, const uint8_t *hq
 
 /* fp64 dot of one MXFP4 row with MXFP8-quantized activations. */
 static double mx_row_mx8(const uint8_t *p, const uint8_t *s, const uint8_t *xq,
-                         const uint8_t *xs, uint32_t cols) {
+                         const uint8_t *xs, uint32_t cols, uint32_t sblk) {
     double acc = 0.0;
     for (uint32_t c = 0; c < cols; c++)
         acc += (double)nib(p, c) * (double)k3o_e8m0(s[c / 32u]) *
-               (double)k3o_e4m3(xq[c]) * (double)k3o_e8m0(xs[c / 32u]);
+               (double)k3o_e4m3(xq[c]) * (double)k3o_e8m0(xs[c / sblk]);
     return acc;
 }
 
@@ -796,8 +824,8 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
                     const uint32_t t = token_list ? token_list[i] : (uint32_t)i;
                     const uint16_t *x = hidden_in + (uint64_t)t * H;
                     const uint64_t o = (uint64_t)i * H;
-                    if (ord == 3) k3o_mx8_quantize(xq + o, xs + o / 32u, x, H);
-                    else k3o_mx8_split(xq + o, xs + o / 32u, xq2 + o, xs2 + o / 32u, x, H);
+                    if (ord == 3) k3o_mx8_quantize_rows(xq + o, xs + i, x, 1u, H);
+                    else k3o_mx8_split_rows(xq + o, xs + i, xq2 + o, xs2 + i, x, 1u, H);
                 }
             }
 #pragma omp parallel for schedule(dynamic, 1)
@@ -818,13 +846,13 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
                         vg = mx_row_ref128(ex->w1_packed + po, ex->w1_scales + so, x, H);
                         vu = mx_row_ref128(ex->w3_packed + po, ex->w3_scales + so, x, H);
                     } else if (ord == 3) {
-                        vg = (float)mx_row_mx8(ex->w1_packed + po, ex->w1_scales + so, xq + xo, xs + xo / 32u, H);
-                        vu = (float)mx_row_mx8(ex->w3_packed + po, ex->w3_scales + so, xq + xo, xs + xo / 32u, H);
+                        vg = (float)mx_row_mx8(ex->w1_packed + po, ex->w1_scales + so, xq + xo, xs + i, H, H);
+                        vu = (float)mx_row_mx8(ex->w3_packed + po, ex->w3_scales + so, xq + xo, xs + i, H, H);
                     } else if (ord == 4) {
-                        vg = (float)mx_row_split(ex->w1_packed + po, ex->w1_scales + so, xq + xo, xs + xo / 32u,
-                                                 xq2 + xo, xs2 + xo / 32u, H);
-                        vu = (float)mx_row_split(ex->w3_packed + po, ex->w3_scales + so, xq + xo, xs + xo / 32u,
-                                                 xq2 + xo, xs2 + xo / 32u, H);
+                        vg = (float)mx_row_split(ex->w1_packed + po, ex->w1_scales + so, xq + xo, xs + i,
+                                                 xq2 + xo, xs2 + i, H, H);
+                        vu = (float)mx_row_split(ex->w3_packed + po, ex->w3_scales + so, xq + xo, xs + i,
+                                                 xq2 + xo, xs2 + i, H, H);
                     } else {
                         vg = (float)mx_row_f64(ex->w1_packed + po, ex->w1_scales + so, x, H);
                         vu = (float)mx_row_f64(ex->w3_packed + po, ex->w3_scales + so, x, H);
@@ -852,9 +880,9 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
                     float v;
                     if (ord == 0) v = mx_row_w64(ex->w2_packed + po, ex->w2_scales + so, a + ao, F);
                     else if (ord == 1) v = mx_row_ref128(ex->w2_packed + po, ex->w2_scales + so, a + ao, F);
-                    else if (ord == 3) v = (float)mx_row_mx8(ex->w2_packed + po, ex->w2_scales + so, aq + ao, as + ao / 32u, F);
+                    else if (ord == 3) v = (float)mx_row_mx8(ex->w2_packed + po, ex->w2_scales + so, aq + ao, as + ao / 32u, F, 32u);
                     else if (ord == 4) v = (float)mx_row_split(ex->w2_packed + po, ex->w2_scales + so, aq + ao, as + ao / 32u,
-                                                               aq2 + ao, as2 + ao / 32u, F);
+                                                               aq2 + ao, as2 + ao / 32u, F, 32u);
                     else v = (float)mx_row_f64(ex->w2_packed + po, ex->w2_scales + so, a + ao, F);
                     y[row] = k3o_f32_to_bf16(v);
                 }

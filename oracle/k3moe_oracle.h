@@ -135,9 +135,11 @@ typedef struct {
  * expert_out (optional) receives [tokens, top_k, hidden] bf16 slot outputs.
  * gemv_order: 0 = w64, 1 = reference lane order, 2 = fp64, 3 = MX8 (the
  * expert inputs -- x for gate/up, the activation for down -- quantized to
- * MXFP8 by k3o_mx8_quantize, products accumulated in fp64; same bf16
- * rounding points as the other orders), 4 = split MX8 (inputs as the
- * two-term k3o_mx8_split reconstruction hi + lo, fp64 accumulation).
+ * MXFP8, products accumulated in fp64; same bf16 rounding points as the
+ * other orders), 4 = split MX8 (inputs as the two-term hi + lo
+ * reconstruction, fp64 accumulation). x is encoded with one scale per
+ * token row (k3o_mx8_quantize_rows / k3o_mx8_split_rows), the activation
+ * with one per 32 columns (k3o_mx8_quantize / k3o_mx8_split).
  * Returns 0 on success, -1 when a selected expert has no weights.
  */
 int k3o_layer(const k3o_shape *shape, uint32_t tokens,
@@ -156,6 +158,11 @@ uint8_t k3o_f32_to_e4m3(float v);
 void    k3o_mx8_quantize(uint8_t *q, uint8_t *scales, const uint16_t *src, uint64_t n);
 void    k3o_mx8_split(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
                       const uint16_t *src, uint64_t n);
+/* the same encodings with one scale per row of a [rows, cols] matrix */
+void    k3o_mx8_quantize_rows(uint8_t *q, uint8_t *scales, const uint16_t *src, uint64_t rows,
+                              uint64_t cols);
+void    k3o_mx8_split_rows(uint8_t *hi_q, uint8_t *hi_s, uint8_t *lo_q, uint8_t *lo_s,
+                           const uint16_t *src, uint64_t rows, uint64_t cols);
 
 /* ---- prefill byte ledger (k3_prefill.c:136-234, 236-446) ---------------- */
 typedef struct {

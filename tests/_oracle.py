@@ -72,6 +72,8 @@ def lib():
             "k3o_f32_to_e4m3": (ctypes.c_uint8, [_f]),
             "k3o_mx8_quantize": (None, [_p, _p, _p, _u64]),
             "k3o_mx8_split": (None, [_p, _p, _p, _p, _p, _u64]),
+            "k3o_mx8_quantize_rows": (None, [_p, _p, _p, _u64, _u64]),
+            "k3o_mx8_split_rows": (None, [_p, _p, _p, _p, _p, _u64, _u64]),
             "k3o_q8_quantize": (None, [_p, _p, _p, _u32, _u32]),
             "k3o_q8_dequantize": (None, [_p, _p, _p, _u32, _u32]),
             "k3o_q8_gemm": (None, [_p, _p, _p, _p, _p, _u32, _u32, _u32, _i]),
@@ -283,6 +285,30 @@ def mx8_split(x_bf16):
     hs, ls = np.empty(sh, np.uint8), np.empty(sh, np.uint8)
     lib().k3o_mx8_split(_ptr(hq), _ptr(hs), _ptr(lq), _ptr(ls), _ptr(x), x.size)
     return hq, hs, lq, ls
+
+
+def mx8_quantize_rows(x_bf16):
+    """bf16 bits [rows, cols] -> (E4M3 codes, one E8M0 scale per row)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty(x.shape[0], np.uint8)
+    lib().k3o_mx8_quantize_rows(_ptr(q), _ptr(s), _ptr(x), x.shape[0], x.shape[1])
+    return q, s
+
+
+def mx8_split_rows(x_bf16):
+    """bf16 bits [rows, cols] -> (hi codes, hi row scales, lo codes, lo row scales)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    hq, lq = np.empty(x.shape, np.uint8), np.empty(x.shape, np.uint8)
+    hs, ls = np.empty(x.shape[0], np.uint8), np.empty(x.shape[0], np.uint8)
+    lib().k3o_mx8_split_rows(_ptr(hq), _ptr(hs), _ptr(lq), _ptr(ls), _ptr(x), x.shape[0],
+                             x.shape[1])
+    return hq, hs, lq, ls
+
+
+def mx8_dequantize_rows(q, s):
+    t = e4m3_table().astype(np.float64)
+    return t[q] * np.ldexp(1.0, s.astype(np.int64) - 127)[:, None]
 
 
 def mx8_dequantize(q, s):

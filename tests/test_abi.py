@@ -64,6 +64,7 @@ def test_workspace_sizes_and_validation():
                                      None)
     assert not L.k3_rocm_mxfp4_gemv_bf16(None, None, None, None, 16, 64, None)
     assert not L.k3_moe_mx8_quantize_bf16(None, None, None, None, None, 32, None)
+    assert not L.k3_moe_mx8_quantize_rows_bf16(None, None, None, None, None, 1, 32, None)
 
 
 def test_router_scratch_sizes_and_validation():

@@ -119,6 +119,52 @@ def test_mx8_quantize_bitexact(cuda):
     assert not lib().k3_moe_mx8_quantize_bf16(P(hq), P(hs), P(lq), None, P(src), n, st)
 
 
+@pytest.mark.parametrize("cols", [7168, 2048, 520])
+def test_mx8_quantize_rows_bitexact(cuda, cols):
+    """Per-row scales (the token rows of the gate/up products) against the
+    oracle's k3o_mx8_split_rows / k3o_mx8_quantize_rows."""
+    rng = np.random.default_rng(22 + cols)
+    rows = 96
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * np.ldexp(
+        1.0, rng.integers(-60, 60, (rows, 1)))
+    x[:, ::5] *= np.ldexp(1.0, rng.integers(-30, 0, (rows, (cols + 4) // 5)))
+    x[0] = 0.0
+    x[1] = 1e-39
+    x[2] *= np.float32(6.5e4)
+    x[3, 100], x[3, 7] = np.inf, -np.inf        # +-inf among finite values
+    x[4, 17] = np.nan                           # NaN among finite values
+    x[5] = np.float32(2.0 ** -133)              # maximum below 2^-119: scale byte 0
+    xb = f32_to_bf16_bits(x)
+    # rows of every bf16 value within +-448 behind a 448 marker (row scale
+    # 2^0: each value encoded as itself)
+    pos = np.arange(0x0000, 0x43E1, dtype=np.uint32)
+    sweep = np.concatenate([pos, pos | 0x8000]).astype(np.uint16)
+    per = cols - 1
+    sweep = np.concatenate([sweep, np.zeros((-sweep.size) % per, np.uint16)]).reshape(-1, per)
+    marker = np.full((sweep.shape[0], 1), 0x43E0, np.uint16)
+    xb = np.concatenate([xb, np.concatenate([marker, sweep], axis=1)])
+    rows = xb.shape[0]
+    src = torch.from_numpy(xb.view(np.int16)).to(cuda)
+    hq = torch.empty((rows, cols), dtype=torch.uint8, device=cuda)
+    lq = torch.empty_like(hq)
+    hs = torch.empty(rows, dtype=torch.uint8, device=cuda)
+    ls = torch.empty_like(hs)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib().k3_moe_mx8_quantize_rows_bf16(P(hq), P(hs), P(lq), P(ls), P(src), rows, cols, st)
+    torch.cuda.synchronize()
+    for got, exp in zip((hq, hs, lq, ls), O.mx8_split_rows(xb)):
+        np.testing.assert_array_equal(got.cpu().numpy(), exp)
+    assert lib().k3_moe_mx8_quantize_rows_bf16(P(hq), P(hs), None, None, P(src), rows, cols, st)
+    torch.cuda.synchronize()
+    q1, s1 = O.mx8_quantize_rows(xb)
+    np.testing.assert_array_equal(hq.cpu().numpy(), q1)
+    np.testing.assert_array_equal(hs.cpu().numpy(), s1)
+    assert not lib().k3_moe_mx8_quantize_rows_bf16(P(hq), P(hs), None, None, P(src), rows, 12, st)
+    assert not lib().k3_moe_mx8_quantize_rows_bf16(P(hq), P(hs), P(lq), None, P(src), rows, cols,
+                                                   st)
+
+
 def small_cfg(tokens):
     """Config 0's shape (H 2048, 64 experts, top-4, F 512) with a batch."""
     return dataclasses.replace(CONFIGS[0], name=f"cfg0x{tokens}", tokens=tokens)

@@ -294,6 +294,61 @@ def test_mx8_quantize_block_invariants_and_torch():
     assert np.all(np.abs(deq - xf) <= step / 2)
 
 
+def test_mx8_rows_invariants_and_torch():
+    """One scale per row: the block rule over the whole row, codes from
+    torch's E4M3 cast of x * 2^-X."""
+    rng = np.random.default_rng(13)
+    rows, cols = 512, 7168
+    mag = np.ldexp(1.0, rng.integers(-40, 40, rows))[:, None]
+    x = (rng.standard_normal((rows, cols)) * mag).astype(np.float32)
+    x[:, :64] *= np.ldexp(1.0, rng.integers(-20, 1, (rows, 64)))  # spread within rows
+    x[5] = 0.0
+    x[6] = 0.0
+    x[6, 3] = 1e-39
+    xb = f32_to_bf16_bits(x)
+    xf = bf16_bits_to_f32(xb).astype(np.float64)
+    q, s = O.mx8_quantize_rows(xb)
+    X = s.astype(np.int64) - 127
+    amax = np.abs(xf).max(axis=1)
+    nz = (amax > 0) & (X > -127)
+    r = amax[nz] * np.ldexp(1.0, -X[nz])
+    assert np.all((r > 224) & (r <= 448))
+    assert np.all((r >= 256) | (amax[nz] * np.ldexp(1.0, -X[nz] + 1) > 448))
+    assert X[6] == -127 and s[5] == 0 and np.all(q[5] == 0)
+    scaled = np.clip(xf * np.ldexp(1.0, -X)[:, None], -448, 448).astype(np.float32)
+    want = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(q, want)
+    # a 32-column row is one block of the per-block encoding
+    q32, s32 = O.mx8_quantize(xb[:, :32])
+    q32r, s32r = O.mx8_quantize_rows(np.ascontiguousarray(xb[:, :32]))
+    np.testing.assert_array_equal(q32r, q32)
+    np.testing.assert_array_equal(s32r, s32[:, 0])
+
+
+def test_mx8_split_rows_reconstructs_bf16():
+    rng = np.random.default_rng(14)
+    rows, cols = 256, 7168
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * np.ldexp(1.0, rng.integers(
+        -30, 30, (rows, 1)))
+    x[:, ::7] *= np.ldexp(1.0, rng.integers(-24, 0, (rows, (cols + 6) // 7)))
+    x[3] = 0.0
+    xb = f32_to_bf16_bits(x)
+    xf = bf16_bits_to_f32(xb).astype(np.float64)
+    hq, hs, lq, ls = O.mx8_split_rows(xb)
+    rec = O.mx8_dequantize_rows(hq, hs) + O.mx8_dequantize_rows(lq, ls)
+    top = np.abs(xf).max(axis=1, keepdims=True)
+    # exact for elements within 2^-6 of the row maximum ...
+    near = np.abs(xf) >= top * 2.0 ** -6
+    np.testing.assert_array_equal(rec[near], xf[near])
+    # ... and within 2^-22 of the row maximum for every element
+    assert np.all(np.abs(rec - xf) <= top * 2.0 ** -22)
+    assert hs[3] == 0 and np.all(hq[3] == 0) and np.all(lq[3] == 0)
+    # the hi term alone is the one-term encoding
+    q1, s1 = O.mx8_quantize_rows(xb)
+    np.testing.assert_array_equal(hq, q1)
+    np.testing.assert_array_equal(hs, s1)
+
+
 def test_mx8_layer_close_to_exact_layer():
     cfg = CONFIGS[0]
     inputs = make_inputs(cfg)
