@@ -311,7 +311,11 @@ struct TileCfg {
     /* E8M0 scales live outside the stages, in two scale buffers: a scale
      * block holds 16 bytes of every row (SQ stages' worth, 4 scales per 128
      * K), so a row's scales arrive in one 16-byte request per SQ stages
-     * instead of a 4-byte request per stage. Chunk = 64 rows x 16 B. */
+     * instead of a 4-byte request per stage. Chunk = 64 rows x 16 B. With
+     * SBH = 2 a scale block holds two such 16-byte records per weight row
+     * (the row's next 32 bytes, fetched together: one touch per scale line
+     * in half as many blocks), the second in a second SB region. */
+    static constexpr int SBH = 1;
     static constexpr int SQ = 4 / KS;
     static constexpr int SA_ROWS = (BM + 63) / 64 * 64; /* whole 64-row scale chunks */
     static constexpr int SA_CH = TERMS * SA_ROWS / 64, SB_CH = BN / 64;
@@ -345,8 +349,12 @@ struct TileCfg {
 template <class C>
 struct RowScaled : C {
     static constexpr bool AROW = true;
-    static constexpr int SA_CH = 0, OFF_SA = 0, OFF_SB = 0, SBUF = C::SB_CH * 1024;
+    /* the freed activation scale space takes weight scale blocks of two
+     * records per row */
+    static constexpr int SBH = 2, SQ = SBH * 4 / C::KS;
+    static constexpr int SA_CH = 0, OFF_SA = 0, OFF_SB = 0, SBUF = SBH * C::SB_CH * 1024;
     static constexpr int LDS = C::STAGE * C::STAGES + 2 * SBUF;
+    static_assert(LDS <= 160 * 1024, "LDS");
     using DSA = Deal<0, C::NWV>;
 };
 
@@ -377,6 +385,7 @@ struct Loader {
     const uint8_t *sb[C::DSB::per > 0 ? C::DSB::per : 1];
     uint32_t mask;      /* kinds held: bit 3 A, 2 B, 1 SA, 0 SB */
     uint32_t sa_stride; /* bytes between consecutive scale blocks of an SA row */
+    uint32_t sb_recs;   /* 16-byte scale records per weight row (K / 512) */
 };
 
 /* chunk index of slot q of a kind for this wave */
@@ -407,7 +416,11 @@ __device__ __forceinline__ void issue_step(const Loader<C> &L, uint8_t *stage, u
         if (L.mask & 1u) {
 #pragma unroll
             for (int q = 0; q < C::DSB::per; q++)
-                dma<16>(L.sb[q] + 16u * b, sbuf + C::OFF_SB + 1024 * chunk_of<typename C::DSB, W>(q, wave));
+#pragma unroll
+                for (int h = 0; h < C::SBH; h++)
+                    if (h == 0 || C::SBH * b + (uint32_t)h < L.sb_recs) /* not past the row */
+                    dma<16>(L.sb[q] + 16u * (C::SBH * b + (uint32_t)h),
+                            sbuf + C::OFF_SB + 1024 * (h * C::SB_CH + chunk_of<typename C::DSB, W>(q, wave)));
         }
     }
     if (L.mask & 8u) {
@@ -514,10 +527,12 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
     const uint32_t b_base = C::KS == 2
         ? base + C::OFF_B + a_slot(c, 4u * KSI + g) + 2048u * C::WN * wn
         : base + C::OFF_B + 16u * lane + 1024u * C::WN * wn;
-    /* scales: row r's dword for this K slice at 16 r + 4 (KS sq + KSI) */
-    const uint32_t sbase = lds_addr(sbuf) + 16u * c + 4u * (C::KS * sq + KSI);
+    /* scales: row r's dword for K slice kq at 16 r + 4 (kq % 4) of record
+     * kq / 4 (SB records are regions of SB_CH KB) */
+    const uint32_t kq = C::KS * sq + KSI; /* 128-column slice within the scale block */
+    const uint32_t sbase = lds_addr(sbuf) + 16u * c + 4u * (kq & 3u);
     const uint32_t sa_base = sbase + C::OFF_SA + 256u * C::WM * wm;
-    const uint32_t sb_base = sbase + C::OFF_SB + 256u * C::WN * wn;
+    const uint32_t sb_base = sbase + C::OFF_SB + 1024u * C::SB_CH * (kq >> 2) + 256u * C::WN * wn;
     u32x4_t alo[NA], ahi[NA], bv[C::WN];
     uint32_t saw[NA], sbw[C::WN];
     auto read_a = [&](auto I) {
@@ -936,6 +951,7 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
         }
         static_assert(C::AROW, "gate/up takes per-row activation scales");
         L.sa_stride = 0u;
+        L.sb_recs = H / 512u;
     }
     RowScales<C> rs; /* lane row c of each of the wave's row blocks */
 #pragma unroll
@@ -1028,6 +1044,7 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
         L.sa[q] = A.B.as[t] + prow(r) * 16u;
     }
     L.sa_stride = 16u * A.B.routes; /* scale block b of every row at + b 16 routes */
+    L.sb_recs = F / 512u;
     f32x4 acc[C::WM][C::WN];
 #pragma unroll
     for (int i = 0; i < C::WM; i++)
@@ -1170,7 +1187,8 @@ bool build_tiles_all(const MfmaBuffers &B, const uint32_t *counts, const uint32_
 }
 
 bool mfma_supported(const k3_moe_shape &s) {
-    return s.hidden % 512u == 0u && s.ffn % 256u == 0u && s.expert_count <= 1024u;
+    /* 16-byte scale records: whole ones per row of every weight tensor */
+    return s.hidden % 512u == 0u && s.ffn % 512u == 0u && s.expert_count <= 1024u;
 }
 
 bool mfma_launch_experts(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,

@@ -170,10 +170,13 @@ def small_cfg(tokens):
     return dataclasses.replace(CONFIGS[0], name=f"cfg0x{tokens}", tokens=tokens)
 
 
+@pytest.mark.parametrize("shape", [(2048, 512), (1536, 1536)], ids=["h2048", "h1536"])
 @pytest.mark.parametrize("precision,order", [(MFMA, O.ORDER_SPLIT), (MFMA_FP8, O.ORDER_MX8)],
                          ids=["mfma", "mfma_fp8"])
-def test_small_batch_vs_oracle(cuda, precision, order):
-    cfg = small_cfg(72)
+def test_small_batch_vs_oracle(cuda, precision, order, shape):
+    """H 1536: an odd count of 16-byte scale records per gate/up row (the
+    last two-record scale block holds one)."""
+    cfg = dataclasses.replace(small_cfg(72), hidden=shape[0], ffn=shape[1])
     inputs = make_inputs(cfg, tokens=cfg.tokens)
     moe = get_layer(cfg, inputs, cuda)
     out, ids, w = forward(moe, inputs, cuda, precision)
