@@ -4,8 +4,11 @@
  * launch_prefill_expert (k3_engine_prefill.inc:962-990): one launch per
  * tile-size class covers every selected expert of the layer.
  *
- *   x_split_kernel      hidden rows -> MXFP8 hi (and lo) codes + scales
- *   tile_build_kernel   plan -> per-class tile lists (16/32/64-row tiles)
+ *   x_split_kernel      bf16 values -> MXFP8 hi (and lo) codes + scales per
+ *                       32 (the k3_moe_mx8_quantize_bf16 ABI)
+ *   x_split_rows_kernel token rows -> E4M3 hi (and lo) codes, one scale
+ *                       per row and term
+ *   tile_build_kernel   plan -> per-class tile lists (16/64/96/128-row tiles)
  *   gateup_mfma_kernel  act = bf16(f(bf16(x.Wg), bf16(x.Wu))), written as
  *                       MXFP8 hi/lo of the activation (blocks of 32 along F)
  *   down_mfma_kernel    y[route] = bf16(act . Wd) for the route's slot
@@ -17,9 +20,10 @@
  * Both scale operands are the E8M0 byte of K block g of the lane's row.
  * Output: lane l holds rows 4g + i (i < 4) of column c.
  *
- * Tiles: a block is 4 waves over 256 weight rows and 16, 64 or 128
- * activation rows (by the expert's row count); K advances 128 per step
- * through a 3-stage LDS ring filled by direct-to-LDS loads.
+ * Tiles: by the expert's row count, a block computes 16, 64, 96 or 128
+ * activation rows against 128, 256 or 512 weight rows with 2 to 8 waves
+ * (the Cls* configurations below); K advances 128 or 256 per step through
+ * a 2- or 3-stage LDS ring filled by direct-to-LDS loads.
  */
 #include "k3_device.h"
 #include "k3_mfma.h"
@@ -1088,11 +1092,8 @@ using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2, 2>;
 /* 128 x 512 blocks: eight waves, two per SIMD, each 64 activation rows x
  * 128 weight rows; halves the activation re-reads of a 256-wide block, two
  * stage buffers */
-#ifndef K3_C3
-#define K3_C3 2, 4, 4, 8, TERMS, 2
-#endif
 template <int TERMS>
-using Cls3 = TileCfg<K3_C3>;
+using Cls3 = TileCfg<2, 4, 4, 8, TERMS, 2>;
 /* 96 x 512 blocks for experts of 65-96 rows, one tile each (most experts
  * of a Zipf batch's 128-row range): a quarter less activation staging per
  * K step than a padded 128-row tile, 48 rows per wave. One term stages
@@ -1102,10 +1103,7 @@ using Cls3 = TileCfg<K3_C3>;
 #define K3_C2_AUX 0
 #endif
 template <int TERMS>
-#ifndef K3_C2
-#define K3_C2 2, 4, 3, 8, 2, 2, 1, K3_C2_AUX
-#endif
-using Cls2 = std::conditional_t<TERMS == 2, TileCfg<K3_C2>, Cls3<TERMS>>;
+using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, K3_C2_AUX>, Cls3<TERMS>>;
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
