@@ -63,7 +63,7 @@ def test_native_k3_decode_bitexact(cuda):
 def test_native_mfma_close_to_exact(cuda):
     """MFMA expert products inside the native layer: routes stay exact; the
     output is within the MFMA precision's stated bound of the exact one."""
-    cfg = N.NativeConfig("native-mfma", 40, 1024, 512, 64, 4, 256, 768, seed=2003)
+    cfg = N.NativeConfig("native-mfma", 40, 1024, 512, 64, 4, 512, 768, seed=2003)
     layer = N.NativeLayer(cfg, device=cuda)
     got, want, _ = run_and_check(cfg, 40, cuda, layer=layer, precision=1, residual=False)
     gf = (got.astype(np.uint32) << 16).view(np.float32)
@@ -78,7 +78,7 @@ def test_native_mfma_projections_close_to_exact(cuda, kind):
     bf16 MFMA too (exact products, another fp32 summation order). Routes
     stay exact; the output is within the MFMA precision's bound."""
     T = 300
-    cfg = N.NativeConfig("native-proj", T, 1024, 512, 64, 4, 256, 768, static_kind=kind,
+    cfg = N.NativeConfig("native-proj", T, 1024, 512, 64, 4, 512, 768, static_kind=kind,
                          seed=2100 + kind)
     got, want, _ = run_and_check(cfg, T, cuda, precision=1)
     gf = (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
