@@ -122,16 +122,25 @@ Workspace carve(void *base, const k3_moe_shape &s, uint32_t T) {
 /* ------------------------------------------------------------------------ */
 
 /* Route (t, r) is valid when its id is < E and no earlier rank of token t
- * chose the same expert (the router never does; external ids might). */
-__device__ __forceinline__ bool route_valid(const uint32_t *ids, uint32_t t, uint32_t r,
-                                            uint32_t k, uint32_t E) {
-    const uint32_t e = ids[(uint64_t)t * k + r];
-    if (e >= E) return false;
-    for (uint32_t q = 0; q < r; q++)
-        if (ids[(uint64_t)t * k + q] == e) return false;
-    return true;
+ * chose the same expert (the router never does; external ids might). The
+ * token's k <= K ids are read once into registers (all loads issued
+ * together); invalid routes come back as E. A later duplicate matches the
+ * first occurrence, which stays, so invalidating in place keeps the rule. */
+template <int K>
+__device__ __forceinline__ void token_routes(const uint32_t *ids, uint32_t t, uint32_t k,
+                                             uint32_t E, uint32_t (&e)[K]) {
+#pragma unroll
+    for (int r = 0; r < K; r++) e[r] = (uint32_t)r < k ? ids[(uint64_t)t * k + r] : E;
+#pragma unroll
+    for (int r = 0; r < K; r++) {
+        if (e[r] >= E) e[r] = E;
+#pragma unroll
+        for (int q = 0; q < r; q++)
+            if (e[q] == e[r]) e[r] = E;
+    }
 }
 
+template <int K>
 __global__ __launch_bounds__(256) void plan_count_kernel(uint32_t *__restrict__ chunk_counts,
                                                          const uint32_t *__restrict__ ids,
                                                          uint32_t T, uint32_t k, uint32_t E) {
@@ -139,9 +148,13 @@ __global__ __launch_bounds__(256) void plan_count_kernel(uint32_t *__restrict__ 
     for (uint32_t e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0u;
     __syncthreads();
     const uint32_t t = blockIdx.x * kPlanChunk + threadIdx.x;
-    if (t < T)
-        for (uint32_t r = 0; r < k; r++)
-            if (route_valid(ids, t, r, k, E)) atomicAdd(&hist[ids[(uint64_t)t * k + r]], 1u);
+    if (t < T) {
+        uint32_t e[K];
+        token_routes<K>(ids, t, k, E, e);
+#pragma unroll
+        for (int r = 0; r < K; r++)
+            if (e[r] < E) atomicAdd(&hist[e[r]], 1u);
+    }
     __syncthreads();
     for (uint32_t e = threadIdx.x; e < E; e += blockDim.x)
         chunk_counts[(uint64_t)blockIdx.x * E + e] = hist[e];
@@ -198,6 +211,7 @@ __global__ __launch_bounds__(1024) void plan_scan_kernel(
     }
 }
 
+template <int K>
 __global__ __launch_bounds__(256) void plan_scatter_kernel(
         uint32_t *__restrict__ token_index, uint32_t *__restrict__ route_index,
         const uint32_t *__restrict__ chunk_base, const uint32_t *__restrict__ ids, uint32_t T,
@@ -207,21 +221,24 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
     __syncthreads();
     const uint32_t t = blockIdx.x * kPlanChunk + threadIdx.x;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    if (t < T)
-        for (uint32_t r = 0; r < k; r++)
-            if (route_valid(ids, t, r, k, E))
-                atomicOr(&masks[wave][ids[(uint64_t)t * k + r]], 1ull << lane);
+    uint32_t e[K];
+    if (t < T) {
+        token_routes<K>(ids, t, k, E, e);
+#pragma unroll
+        for (int r = 0; r < K; r++)
+            if (e[r] < E) atomicOr(&masks[wave][e[r]], 1ull << lane);
+    }
     __syncthreads();
     if (t >= T) return;
     const unsigned long long below = (1ull << lane) - 1ull;
-    for (uint32_t r = 0; r < k; r++) {
-        if (!route_valid(ids, t, r, k, E)) continue;
-        const uint32_t e = ids[(uint64_t)t * k + r];
-        uint32_t before = (uint32_t)__popcll(masks[wave][e] & below);
-        for (uint32_t w = 0; w < wave; w++) before += (uint32_t)__popcll(masks[w][e]);
-        const uint32_t pos = chunk_base[(uint64_t)blockIdx.x * E + e] + before;
+#pragma unroll
+    for (int r = 0; r < K; r++) {
+        if (e[r] >= E) continue;
+        uint32_t before = (uint32_t)__popcll(masks[wave][e[r]] & below);
+        for (uint32_t w = 0; w < wave; w++) before += (uint32_t)__popcll(masks[w][e[r]]);
+        const uint32_t pos = chunk_base[(uint64_t)blockIdx.x * E + e[r]] + before;
         token_index[pos] = t;
-        route_index[pos] = t * k + r;
+        route_index[pos] = t * k + (uint32_t)r;
     }
 }
 
@@ -229,12 +246,20 @@ bool launch_plan(uint32_t *counts, uint32_t *offsets, uint32_t *unique, uint32_t
                  uint32_t *token_index, uint32_t *route_index, uint32_t *chunk_base,
                  const uint32_t *ids, uint32_t T, uint32_t k, uint32_t E, hipStream_t s) {
     const uint32_t chunks = (T + kPlanChunk - 1u) / kPlanChunk;
-    hipLaunchKernelGGL(plan_count_kernel, dim3(chunks), dim3(kPlanChunk), 0, s, chunk_base, ids,
-                       T, k, E);
+    if (k <= 16u)
+        hipLaunchKernelGGL(plan_count_kernel<16>, dim3(chunks), dim3(kPlanChunk), 0, s, chunk_base,
+                           ids, T, k, E);
+    else
+        hipLaunchKernelGGL(plan_count_kernel<32>, dim3(chunks), dim3(kPlanChunk), 0, s, chunk_base,
+                           ids, T, k, E);
     hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(1024), 0, s, chunk_base, counts, offsets,
                        unique, summary, chunks, E, T * k);
-    hipLaunchKernelGGL(plan_scatter_kernel, dim3(chunks), dim3(kPlanChunk), 0, s, token_index,
-                       route_index, chunk_base, ids, T, k, E);
+    if (k <= 16u)
+        hipLaunchKernelGGL(plan_scatter_kernel<16>, dim3(chunks), dim3(kPlanChunk), 0, s,
+                           token_index, route_index, chunk_base, ids, T, k, E);
+    else
+        hipLaunchKernelGGL(plan_scatter_kernel<32>, dim3(chunks), dim3(kPlanChunk), 0, s,
+                           token_index, route_index, chunk_base, ids, T, k, E);
     return hipGetLastError() == hipSuccess;
 }
 
