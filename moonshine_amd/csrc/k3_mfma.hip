@@ -129,52 +129,106 @@ __device__ __forceinline__ void bf16x8_to_f32(uint4 p, float (&v)[8]) {
  * One block of 256 threads per token row of [T, H] bf16 (H % 8 == 0): the
  * row's E4M3 codes under one E8M0 scale per term (the scale rule of the
  * 32-element MXFP8 blocks applied to the whole row), hi and, for two
- * terms, lo = x - hi under its own scale. The row is read once per pass
- * (maximum, residual maximum, codes); after the first it comes from L2.
- * With one scale per row the MFMA lanes hold their rows' scales in
- * registers for the whole K loop instead of staging scale bytes per step.
+ * terms, lo = x - hi under its own scale. With M > 0 (H <= 2048 M) each
+ * thread keeps its M chunks of 8 values in registers and the row is read
+ * once; M = 0 reads it once per pass (maximum, residual maximum, codes),
+ * from L2 after the first. With one scale per row the MFMA lanes hold
+ * their rows' scales in registers for the whole K loop instead of staging
+ * scale bytes per step.
  */
-template <int TERMS>
+template <int TERMS, int M>
 __global__ __launch_bounds__(256) void x_split_rows_kernel(MfmaBuffers B,
                                                            const uint16_t *__restrict__ x,
                                                            uint32_t H) {
     __shared__ float red[4];
     const uint32_t row = blockIdx.x, chunks = H / 8u;
     const uint4 *src = (const uint4 *)(x + (uint64_t)row * H);
-    float amax = 0.0f;
-    for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
-        float v[8];
-        bf16x8_to_f32(src[q], v);
+    uint2 *hq = (uint2 *)(B.xq[0] + (uint64_t)row * H);
+    uint2 *lq = (uint2 *)(B.xq[TERMS - 1] + (uint64_t)row * H);
+    uint32_t s0, s1 = 0u;
+    if constexpr (M > 0) {
+        float v[M][8];
+        bool live[M];
 #pragma unroll
-        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
-    }
-    const uint32_t s0 = mx8_scale_byte(block_max256(amax, red));
-    const float inv0 = mx8_inv_scale(s0), sc0 = e8m0_to_f32(s0);
-    uint32_t s1 = 0u;
-    if constexpr (TERMS == 2) {
-        float rmax = 0.0f;
+        for (int m = 0; m < M; m++) {
+            const uint32_t q = threadIdx.x + 256u * (uint32_t)m;
+            live[m] = q < chunks;
+            bf16x8_to_f32(live[m] ? src[q] : make_uint4(0u, 0u, 0u, 0u), v[m]);
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[m][i]));
+        s0 = mx8_scale_byte(block_max256(amax, red));
+        const float inv0 = mx8_inv_scale(s0), sc0 = e8m0_to_f32(s0);
+        uint2 h[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) h[m] = e4m3x8<TERMS == 2>(v[m], inv0, sc0);
+        if constexpr (TERMS == 2) {
+            float rmax = 0.0f; /* padding chunks hold zeros: residual 0 */
+#pragma unroll
+            for (int m = 0; m < M; m++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) rmax = fmaxf(rmax, fabsf(v[m][i]));
+            s1 = mx8_scale_byte(block_max256(rmax, red));
+        }
+        const float inv1 = mx8_inv_scale(s1);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (!live[m]) continue;
+            const uint32_t q = threadIdx.x + 256u * (uint32_t)m;
+            hq[q] = h[m];
+            if constexpr (TERMS == 2) lq[q] = e4m3x8<false>(v[m], inv1, 0.0f);
+        }
+    } else {
+        float amax = 0.0f;
         for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
             float v[8];
             bf16x8_to_f32(src[q], v);
-            (void)e4m3x8<true>(v, inv0, sc0);
 #pragma unroll
-            for (int i = 0; i < 8; i++) rmax = fmaxf(rmax, fabsf(v[i]));
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
         }
-        s1 = mx8_scale_byte(block_max256(rmax, red));
-    }
-    const float inv1 = mx8_inv_scale(s1);
-    uint2 *hq = (uint2 *)(B.xq[0] + (uint64_t)row * H);
-    uint2 *lq = (uint2 *)(B.xq[TERMS - 1] + (uint64_t)row * H);
-    for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
-        float v[8];
-        bf16x8_to_f32(src[q], v);
-        hq[q] = e4m3x8<TERMS == 2>(v, inv0, sc0);
-        if constexpr (TERMS == 2) lq[q] = e4m3x8<false>(v, inv1, 0.0f);
+        s0 = mx8_scale_byte(block_max256(amax, red));
+        const float inv0 = mx8_inv_scale(s0), sc0 = e8m0_to_f32(s0);
+        if constexpr (TERMS == 2) {
+            float rmax = 0.0f;
+            for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
+                float v[8];
+                bf16x8_to_f32(src[q], v);
+                (void)e4m3x8<true>(v, inv0, sc0);
+#pragma unroll
+                for (int i = 0; i < 8; i++) rmax = fmaxf(rmax, fabsf(v[i]));
+            }
+            s1 = mx8_scale_byte(block_max256(rmax, red));
+        }
+        const float inv1 = mx8_inv_scale(s1);
+        for (uint32_t q = threadIdx.x; q < chunks; q += 256u) {
+            float v[8];
+            bf16x8_to_f32(src[q], v);
+            hq[q] = e4m3x8<TERMS == 2>(v, inv0, sc0);
+            if constexpr (TERMS == 2) lq[q] = e4m3x8<false>(v, inv1, 0.0f);
+        }
     }
     if (threadIdx.x == 0u) {
         B.xs[0][row] = (uint8_t)s0;
         if constexpr (TERMS == 2) B.xs[1][row] = (uint8_t)s1;
     }
+}
+
+/* x_split_rows_kernel<TERMS, M> for H: registers up to H = 8192. */
+template <int TERMS>
+void launch_split_rows(const MfmaBuffers &B, const uint16_t *x, uint32_t rows, uint32_t H,
+                       hipStream_t st) {
+    if (H <= 2048u)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<TERMS, 1>), dim3(rows), dim3(256),
+                           0, st, B, x, H);
+    else if (H <= 8192u)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<TERMS, 4>), dim3(rows), dim3(256),
+                           0, st, B, x, H);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<TERMS, 0>), dim3(rows), dim3(256),
+                           0, st, B, x, H);
 }
 
 /* ---------------------------------------------------------------------- */
@@ -1128,8 +1182,7 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
                   const uint32_t *route_index, const k3_moe_expert *experts, const k3_moe_shape &s,
                   uint32_t T, hipStream_t st, const StageMarker &mark) {
     const uint32_t H = s.hidden, F = s.ffn;
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<TERMS>), dim3(T), dim3(256), 0, st, B,
-                       hidden, H);
+    launch_split_rows<TERMS>(B, hidden, T, H, st);
     hipLaunchKernelGGL(tile_build_kernel, dim3(1), dim3(1024), 0, st, B, counts, offsets,
                        experts, s.expert_count, 0u);
     mark(K3_MOE_STAGE_GATE_UP);
@@ -1243,10 +1296,8 @@ extern "C" bool k3_moe_mx8_quantize_rows_bf16(uint8_t *hi_codes, uint8_t *hi_sca
     B.xq[0] = hi_codes; B.xs[0] = hi_scales;
     B.xq[1] = lo_codes; B.xs[1] = lo_scales;
     if (lo_codes)
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<2>), dim3(rows), dim3(256), 0,
-                           (hipStream_t)stream, B, (const uint16_t *)src, cols);
+        launch_split_rows<2>(B, (const uint16_t *)src, rows, cols, (hipStream_t)stream);
     else
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(x_split_rows_kernel<1>), dim3(rows), dim3(256), 0,
-                           (hipStream_t)stream, B, (const uint16_t *)src, cols);
+        launch_split_rows<1>(B, (const uint16_t *)src, rows, cols, (hipStream_t)stream);
     return hipGetLastError() == hipSuccess;
 }

@@ -119,7 +119,7 @@ def test_mx8_quantize_bitexact(cuda):
     assert not lib().k3_moe_mx8_quantize_bf16(P(hq), P(hs), P(lq), None, P(src), n, st)
 
 
-@pytest.mark.parametrize("cols", [7168, 2048, 520])
+@pytest.mark.parametrize("cols", [7168, 2048, 520, 2056, 9000])
 def test_mx8_quantize_rows_bitexact(cuda, cols):
     """Per-row scales (the token rows of the gate/up products) against the
     oracle's k3o_mx8_split_rows / k3o_mx8_quantize_rows."""
