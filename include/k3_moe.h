@@ -59,14 +59,15 @@ typedef enum {
      * between decode and any batch size. */
     K3_MOE_EXACT = 0,
     /* Grouped GEMM on CDNA4 scaled MFMA for token_count > 1: weights stay
-     * MXFP4; each bf16 activation enters as two MXFP8 terms hi + lo (E4M3
-     * codes, one E8M0 scale per 32 values), which reproduce it exactly
-     * except for elements more than 2^6 below their block maximum (error
-     * <= 2^-22 of it). Products are those of the bf16 inputs; accumulation
+     * MXFP4; each bf16 activation enters as two E4M3 terms hi + lo, each
+     * with E8M0 scales (one per token row for the gate/up input, one per
+     * 32 values for the activation that feeds down), which reproduce it
+     * exactly except for elements more than 2^6 below the maximum of their
+     * scale run (error <= 2^-22 of it). Products are those of the bf16 inputs; accumulation
      * is fp32 in MFMA order, so results match EXACT within bf16 tolerance,
      * not bit for bit. One token runs the EXACT decode path. */
     K3_MOE_MFMA = 1,
-    /* As K3_MOE_MFMA with one MXFP8 term (half the MFMA work). Activation
+    /* As K3_MOE_MFMA with one E4M3 term (half the MFMA work). Activation
      * quantisation error is ~4% per element and survives the dot products
      * (~5% relative on expert outputs): an approximate mode, not a
      * drop-in for the reference's numerics. */
