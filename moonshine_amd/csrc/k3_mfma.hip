@@ -806,11 +806,12 @@ __device__ __forceinline__ void mfma_pipeline(f32x4 (&acc)[C::WM][C::WN], const 
  * together as CUs free up and read the tile's activation lines while they
  * are still in L2; with the tile fastest they drifted apart after the
  * first round of blocks (cfg4 gate/up memory reads +9%, layer +2.4%).
- * Returns false for blocks beyond the work count.
+ * L is the block's index in its class's grid (grids are multiples of 8, so
+ * a class placed after another keeps L % 8 = XCD). Returns false for
+ * blocks beyond the work count.
  */
-__device__ __forceinline__ bool xcd_work(uint32_t ntiles, uint32_t cols, uint32_t &tile,
-                                         uint32_t &col) {
-    const uint32_t L = blockIdx.x;
+__device__ __forceinline__ bool xcd_work(uint32_t L, uint32_t ntiles, uint32_t cols,
+                                         uint32_t &tile, uint32_t &col) {
     const uint32_t works = ntiles * cols, per = (works + 7u) / 8u;
     const uint32_t j = L >> 3;
     const uint32_t w = (L & 7u) * per + j;
@@ -932,19 +933,19 @@ __device__ __forceinline__ void gateup_epilogue(const f32x4 (&acc)[C::WM][C::WN]
 }
 
 /*
- * grid xcd_grid(tile cap, F / (BN / 2)), block C::THREADS. The block's
+ * One gate/up block of class C (blk: its index in the class's grid, b0 ..
+ * sbuf1: its LDS ring). The block's
  * BN weight rows are BN / 2 gate rows and the same up rows: wave column wn
  * owns f-columns f0 + 8 WN wn .. + 8 WN, n-subtiles j < WN / 2 gate and
  * j >= WN / 2 up, so gate and up of a column meet in one lane (wrow gives
  * each lane WN / 2 consecutive columns). Epilogue: gateup_epilogue.
  */
 template <class C, uint32_t KIND>
-__global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sbuf0[C::SBUF], sbuf1[C::SBUF];
-    __shared__ __attribute__((aligned(16))) uint8_t b2[C::STAGES == 3 ? C::STAGE : 16];
+__device__ __forceinline__ void gateup_block(const GateUpArgs &A, uint32_t blk, uint8_t *b0,
+                                             uint8_t *b1, uint8_t *b2, uint8_t *sbuf0,
+                                             uint8_t *sbuf1) {
     uint32_t tile, colb;
-    if (!xcd_work(*A.tile_count, A.F / (uint32_t)(C::BN / 2), tile, colb)) return;
+    if (!xcd_work(blk, *A.tile_count, A.F / (uint32_t)(C::BN / 2), tile, colb)) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t wm = wave / C::NW, wn = wave % C::NW;
@@ -1043,14 +1044,13 @@ struct DownArgs {
     uint32_t H, F;
 };
 
-/* grid xcd_grid(tile cap, H / BN), block C::THREADS: y[route] rows d0 .. d0 + BN. */
+/* One down block of class C: y[route] rows d0 .. d0 + BN. */
 template <class C>
-__global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t b0[C::STAGE], b1[C::STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t sbuf0[C::SBUF], sbuf1[C::SBUF];
-    __shared__ __attribute__((aligned(16))) uint8_t b2[C::STAGES == 3 ? C::STAGE : 16];
+__device__ __forceinline__ void down_block(const DownArgs &A, uint32_t blk, uint8_t *b0,
+                                           uint8_t *b1, uint8_t *b2, uint8_t *sbuf0,
+                                           uint8_t *sbuf1) {
     uint32_t tile, colb;
-    if (!xcd_work(*A.tile_count, A.H / (uint32_t)C::BN, tile, colb)) return;
+    if (!xcd_work(blk, *A.tile_count, A.H / (uint32_t)C::BN, tile, colb)) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, c = lane & 15u;
     const uint32_t wm = wave / C::NW, wn = wave % C::NW;
@@ -1159,6 +1159,58 @@ using Cls3 = TileCfg<2, 4, 4, 8, TERMS, 2>;
 template <int TERMS>
 using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, K3_C2_AUX>, Cls3<TERMS>>;
 
+/* LDS of a block running C or D: the ring and scale buffers are distinct
+ * arrays (the pipeline names each buffer statically). */
+template <class C, class D = C>
+struct RingSmem {
+    static constexpr int STAGE = C::STAGE > D::STAGE ? C::STAGE : D::STAGE;
+    static constexpr int SBUF = C::SBUF > D::SBUF ? C::SBUF : D::SBUF;
+    static constexpr bool THREE = C::STAGES == 3 || D::STAGES == 3;
+};
+
+#define K3_RING_SMEM(R)                                                                      \
+    __shared__ __attribute__((aligned(16))) uint8_t b0[R::STAGE], b1[R::STAGE];              \
+    __shared__ __attribute__((aligned(16))) uint8_t sbuf0[R::SBUF], sbuf1[R::SBUF];          \
+    __shared__ __attribute__((aligned(16))) uint8_t b2[R::THREE ? R::STAGE : 16]
+
+/*
+ * gate/up: grid xcd_grid(tile cap, F / (BN / 2)), block C::THREADS. The
+ * block's BN weight rows are BN / 2 gate rows and the same up rows (see
+ * gateup_block).
+ */
+template <class C, uint32_t KIND>
+__global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
+    using R = RingSmem<C>;
+    K3_RING_SMEM(R);
+    gateup_block<C, KIND>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
+}
+
+/* Two tile classes of one block size in one launch: blocks [0, na) run
+ * class C on A's list, the rest class D on B's. The second class's blocks
+ * start while the first's last blocks still run, so the launch has one
+ * tail instead of two (the 96- and 128-row gate/up blocks run ~150 us;
+ * cfg4 gate/up -2%). */
+template <class C, class D, uint32_t KIND>
+__global__ __launch_bounds__(C::THREADS) void gateup_mfma2_kernel(GateUpArgs A, GateUpArgs B,
+                                                                  uint32_t na) {
+    static_assert(C::THREADS == D::THREADS, "one block size");
+    using R = RingSmem<C, D>;
+    K3_RING_SMEM(R);
+    if (blockIdx.x < na)
+        gateup_block<C, KIND>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
+    else
+        gateup_block<D, KIND>(B, blockIdx.x - na, b0, b1, b2, sbuf0, sbuf1);
+}
+
+/* down: grid xcd_grid(tile cap, H / BN), block C::THREADS. */
+template <class C>
+__global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
+    using R = RingSmem<C>;
+    K3_RING_SMEM(R);
+    down_block<C>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
+}
+
+
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
     /* one kernel per activation kind: a kernel holding both epilogues runs
@@ -1175,6 +1227,20 @@ void launch_down(const DownArgs &a, uint32_t cap, hipStream_t st) {
     hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(xcd_grid(cap, a.H / C::BN)),
                        dim3(C::THREADS), 0, st, a);
 }
+
+template <class C, class D>
+void launch_gateup2(const GateUpArgs &a, uint32_t cap_a, const GateUpArgs &b, uint32_t cap_b,
+                    hipStream_t st) {
+    const uint32_t na = xcd_grid(cap_a, a.F / (C::BN / 2));
+    const dim3 grid(na + xcd_grid(cap_b, b.F / (D::BN / 2))), block(C::THREADS);
+    if (a.kind == 1u)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma2_kernel<C, D, 1u>), grid, block, 0, st, a,
+                           b, na);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma2_kernel<C, D, 0u>), grid, block, 0, st, a,
+                           b, na);
+}
+
 
 template <int TERMS>
 bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
@@ -1201,8 +1267,16 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         ga.tile_count = B.tile_count + c;
         if (c == 0) launch_gateup<RowScaled<Cls0G<TERMS>>>(ga, B.tile_cap[c], st);
         if (c == 1) launch_gateup<RowScaled<Cls1<TERMS>>>(ga, B.tile_cap[c], st);
-        if (c == 2) launch_gateup<RowScaled<Cls2<TERMS>>>(ga, B.tile_cap[c], st);
-        if (c == 3) launch_gateup<RowScaled<Cls3<TERMS>>>(ga, B.tile_cap[c], st);
+    }
+    /* classes 3 and 2 (one block size) in one launch: one tail */
+    if (B.tile_cap[3] || B.tile_cap[2]) {
+        GateUpArgs g3 = ga, g2 = ga;
+        g3.tiles = tl[3];
+        g3.tile_count = B.tile_count + 3;
+        g2.tiles = tl[2];
+        g2.tile_count = B.tile_count + 2;
+        launch_gateup2<RowScaled<Cls3<TERMS>>, RowScaled<Cls2<TERMS>>>(g3, B.tile_cap[3], g2,
+                                                                       B.tile_cap[2], st);
     }
     mark(K3_MOE_STAGE_DOWN);
     for (int c = 0; c < kTileClasses; c++) {
@@ -1211,6 +1285,7 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         da.tile_count = B.tile_count + c;
         if (c == 0) launch_down<Cls0<TERMS>>(da, B.tile_cap[c], st);
         if (c == 1) launch_down<Cls1<TERMS>>(da, B.tile_cap[c], st);
+        /* (a paired launch measured level for down, whose blocks are short) */
         if (c == 2) launch_down<Cls2<TERMS>>(da, B.tile_cap[c], st);
         if (c == 3) launch_down<Cls3<TERMS>>(da, B.tile_cap[c], st);
     }
