@@ -430,7 +430,8 @@ def run_layer(args, cfg, T, precision, steps, warmup, R, with_cpu, cpu_budget=No
         kflops = T * cfg.top_k * 2 * 2 * cfg.ffn * cfg.hidden
         achieved = kflops / (kms * 1e-3) / 1e12
         terms = 2 if precision == 1 else 1
-        roofline = {"kernel": "gateup_mfma_kernel", "bound": "mfma", "achieved": achieved,
+        roofline = {"kernel": "gateup_mfma*_kernel (every tile-class launch)", "bound": "mfma",
+                    "achieved": achieved,
                     "peak": MXFP4_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": achieved / MXFP4_PEAK_TFLOPS, "traffic": traffic,
                     "algorithmic_flops": kflops, "avg_ms": kms,
