@@ -246,3 +246,33 @@ def test_tile_class_edges_vs_exact(cuda):
     exact = moe.experts_only(x, ids_d, w_d, residual=r, precision=EXACT)
     torch.cuda.synchronize()
     assert_close(L.bf16_bits(out), L.bf16_bits(exact), "tile class edges mfma vs exact")
+
+
+@pytest.mark.parametrize("T,k,rows", [(70, 1, {7: 70}), (100, 1, {7: 100}),
+                                       (200, 1, {7: 130, 8: 70}), (100, 2, {7: 100, 8: 80})],
+                         ids=["96only", "128only", "128x2+96", "top2"])
+def test_paired_class_launch_edges(cuda, T, k, rows):
+    """The 96- and 128-row classes run in one launch, either part of which
+    may be empty (with R = T k routes the 128-row tile cap is 0 below 97
+    routes): experts routed exactly the listed row counts (rank r of the
+    first tokens), MFMA against the exact path."""
+    cfg = dataclasses.replace(small_cfg(T), top_k=k)
+    inputs = make_inputs(cfg, tokens=T)
+    moe = get_layer(cfg, inputs, cuda)
+    ids = np.full((T, k), 0xFFFFFFFF, np.uint32)
+    used = np.zeros(T, np.int64)
+    for e, n in rows.items():
+        order = np.argsort(used, kind="stable")[:n]  # the tokens with the fewest routes
+        for t in order:
+            ids[t, used[t]] = e
+            used[t] += 1
+    assert used.max() <= k
+    w = np.full(ids.shape, 0.5, np.float32)
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    ids_d = torch.from_numpy(ids.view(np.int32)).to(cuda)
+    w_d = torch.from_numpy(w).to(cuda)
+    out = moe.experts_only(x, ids_d, w_d, residual=r, precision=MFMA)
+    exact = moe.experts_only(x, ids_d, w_d, residual=r, precision=EXACT)
+    torch.cuda.synchronize()
+    assert_close(L.bf16_bits(out), L.bf16_bits(exact), f"paired classes {rows}")
