@@ -1141,8 +1141,11 @@ template <int TERMS>
 using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2, 2>;
 template <int TERMS>
 using Cls0G = TileCfg<1, 2, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2, 2>;
+/* 64 x 256 blocks of eight waves (32 x 64 each, two per SIMD): against four
+ * waves of 64 x 64, cfg4 -1.4%, cfg3 -0.8%; the same block size as the
+ * 96- and 128-row classes, so gate/up launches the three together */
 template <int TERMS>
-using Cls1 = TileCfg<1, 4, 4, 4, TERMS, 2, 2, 2>;
+using Cls1 = TileCfg<2, 4, 2, 4, TERMS, 2, 2, 2>;
 /* 128 x 512 blocks: eight waves, two per SIMD, each 64 activation rows x
  * 128 weight rows; halves the activation re-reads of a 256-wide block, two
  * stage buffers */
@@ -1161,11 +1164,12 @@ using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, K3_C2_A
 
 /* LDS of a block running C or D: the ring and scale buffers are distinct
  * arrays (the pipeline names each buffer statically). */
-template <class C, class D = C>
+template <class C, class D = C, class E = C>
 struct RingSmem {
-    static constexpr int STAGE = C::STAGE > D::STAGE ? C::STAGE : D::STAGE;
-    static constexpr int SBUF = C::SBUF > D::SBUF ? C::SBUF : D::SBUF;
-    static constexpr bool THREE = C::STAGES == 3 || D::STAGES == 3;
+    static constexpr int max3(int a, int b, int c) { return a > b ? (a > c ? a : c) : (b > c ? b : c); }
+    static constexpr int STAGE = max3(C::STAGE, D::STAGE, E::STAGE);
+    static constexpr int SBUF = max3(C::SBUF, D::SBUF, E::SBUF);
+    static constexpr bool THREE = C::STAGES == 3 || D::STAGES == 3 || E::STAGES == 3;
 };
 
 #define K3_RING_SMEM(R)                                                                      \
@@ -1185,21 +1189,24 @@ __global__ __launch_bounds__(C::THREADS) void gateup_mfma_kernel(GateUpArgs A) {
     gateup_block<C, KIND>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
 }
 
-/* Two tile classes of one block size in one launch: blocks [0, na) run
- * class C on A's list, the rest class D on B's. The second class's blocks
- * start while the first's last blocks still run, so the launch has one
- * tail instead of two (the 96- and 128-row gate/up blocks run ~150 us;
- * cfg4 gate/up -2%). */
-template <class C, class D, uint32_t KIND>
-__global__ __launch_bounds__(C::THREADS) void gateup_mfma2_kernel(GateUpArgs A, GateUpArgs B,
-                                                                  uint32_t na) {
-    static_assert(C::THREADS == D::THREADS, "one block size");
-    using R = RingSmem<C, D>;
+/* Three tile classes of one block size in one launch: blocks [0, na) run
+ * class C on A's list, [na, nb) class D on B's, the rest class E on E's.
+ * Each class's blocks start while the previous one's last blocks still run,
+ * so the launch has one tail instead of three (the 96- and 128-row gate/up
+ * blocks run ~150 us; two classes in one launch: cfg4 gate/up -2%). */
+template <class C, class D, class E, uint32_t KIND>
+__global__ __launch_bounds__(C::THREADS) void gateup_mfma3_kernel(GateUpArgs A, GateUpArgs B,
+                                                                  GateUpArgs Ea, uint32_t na,
+                                                                  uint32_t nb) {
+    static_assert(C::THREADS == D::THREADS && C::THREADS == E::THREADS, "one block size");
+    using R = RingSmem<C, D, E>;
     K3_RING_SMEM(R);
     if (blockIdx.x < na)
         gateup_block<C, KIND>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
-    else
+    else if (blockIdx.x < nb)
         gateup_block<D, KIND>(B, blockIdx.x - na, b0, b1, b2, sbuf0, sbuf1);
+    else
+        gateup_block<E, KIND>(Ea, blockIdx.x - nb, b0, b1, b2, sbuf0, sbuf1);
 }
 
 /* down: grid xcd_grid(tile cap, H / BN), block C::THREADS. */
@@ -1228,17 +1235,18 @@ void launch_down(const DownArgs &a, uint32_t cap, hipStream_t st) {
                        dim3(C::THREADS), 0, st, a);
 }
 
-template <class C, class D>
-void launch_gateup2(const GateUpArgs &a, uint32_t cap_a, const GateUpArgs &b, uint32_t cap_b,
-                    hipStream_t st) {
+template <class C, class D, class E>
+void launch_gateup3(const GateUpArgs &a, uint32_t cap_a, const GateUpArgs &b, uint32_t cap_b,
+                    const GateUpArgs &e, uint32_t cap_e, hipStream_t st) {
     const uint32_t na = xcd_grid(cap_a, a.F / (C::BN / 2));
-    const dim3 grid(na + xcd_grid(cap_b, b.F / (D::BN / 2))), block(C::THREADS);
+    const uint32_t nb = na + xcd_grid(cap_b, b.F / (D::BN / 2));
+    const dim3 grid(nb + xcd_grid(cap_e, e.F / (E::BN / 2))), block(C::THREADS);
     if (a.kind == 1u)
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma2_kernel<C, D, 1u>), grid, block, 0, st, a,
-                           b, na);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma3_kernel<C, D, E, 1u>), grid, block, 0, st,
+                           a, b, e, na, nb);
     else
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma2_kernel<C, D, 0u>), grid, block, 0, st, a,
-                           b, na);
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gateup_mfma3_kernel<C, D, E, 0u>), grid, block, 0, st,
+                           a, b, e, na, nb);
 }
 
 
@@ -1266,17 +1274,17 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         ga.tiles = tl[c];
         ga.tile_count = B.tile_count + c;
         if (c == 0) launch_gateup<RowScaled<Cls0G<TERMS>>>(ga, B.tile_cap[c], st);
-        if (c == 1) launch_gateup<RowScaled<Cls1<TERMS>>>(ga, B.tile_cap[c], st);
     }
-    /* classes 3 and 2 (one block size) in one launch: one tail */
-    if (B.tile_cap[3] || B.tile_cap[2]) {
-        GateUpArgs g3 = ga, g2 = ga;
-        g3.tiles = tl[3];
-        g3.tile_count = B.tile_count + 3;
-        g2.tiles = tl[2];
-        g2.tile_count = B.tile_count + 2;
-        launch_gateup2<RowScaled<Cls3<TERMS>>, RowScaled<Cls2<TERMS>>>(g3, B.tile_cap[3], g2,
-                                                                       B.tile_cap[2], st);
+    /* classes 3, 2 and 1 (one block size) in one launch: one tail */
+    if (B.tile_cap[3] || B.tile_cap[2] || B.tile_cap[1]) {
+        GateUpArgs g[kTileClasses];
+        for (int c = 1; c < kTileClasses; c++) {
+            g[c] = ga;
+            g[c].tiles = tl[c];
+            g[c].tile_count = B.tile_count + c;
+        }
+        launch_gateup3<RowScaled<Cls3<TERMS>>, RowScaled<Cls2<TERMS>>, RowScaled<Cls1<TERMS>>>(
+            g[3], B.tile_cap[3], g[2], B.tile_cap[2], g[1], B.tile_cap[1], st);
     }
     mark(K3_MOE_STAGE_DOWN);
     for (int c = 0; c < kTileClasses; c++) {
