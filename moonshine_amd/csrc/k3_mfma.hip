@@ -1118,7 +1118,7 @@ __device__ __forceinline__ void down_block(const DownArgs &A, uint32_t blk, uint
             const uint32_t lr = 16u * (wm * C::WM + (uint32_t)i) + 4u * g + (uint32_t)r;
             if (lr >= rows) continue;
             const uint64_t route = A.route_index[row0 + lr];
-            static_assert(C::WN == 4 || C::WN == 8, "four or eight columns per lane");
+            static_assert(C::WN == 2 || C::WN == 4 || C::WN == 8, "2, 4 or 8 columns per lane");
             uint32_t pk[C::WN / 2];
 #pragma unroll
             for (int j = 0; j < C::WN / 2; j++)
@@ -1127,18 +1127,21 @@ __device__ __forceinline__ void down_block(const DownArgs &A, uint32_t blk, uint
             uint16_t *dst = A.y + route * H + d0 + 16u * C::WN * wn + (uint32_t)C::WN * c;
             if constexpr (C::WN == 8)
                 *(uint4 *)dst = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            else
+            else if constexpr (C::WN == 4)
                 *(uint2 *)dst = make_uint2(pk[0], pk[1]);
+            else
+                *(uint32_t *)dst = pk[0];
         }
 }
 
 /* Tile classes (rows per tile): 16, 64, 96, 128. One-term class 0 computes
  * 32 rows so that its A chunks still split over the waves. Class 0's
  * gate/up takes 128-row weight blocks of two waves (80 KB of LDS: two
- * blocks per CU; cfg2 gate/up 1.68 -> 1.60 ms, cfg3 level); its down keeps
- * 256-row blocks of four waves (measured 3% faster there). */
+ * blocks per CU; cfg2 gate/up 1.68 -> 1.60 ms, cfg3 level); its down
+ * takes 256-row blocks of eight waves of 16 x 32 (two per SIMD: against
+ * four waves of 16 x 64, cfg2 down -11%, cfg3 -5%). */
 template <int TERMS>
-using Cls0 = TileCfg<1, 4, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2, 2>;
+using Cls0 = TileCfg<1, 8, TERMS == 2 ? 1 : 2, 2, TERMS, 3, 2, 2>;
 template <int TERMS>
 using Cls0G = TileCfg<1, 2, TERMS == 2 ? 1 : 2, 4, TERMS, 3, 2, 2>;
 /* 64 x 256 blocks of eight waves (32 x 64 each, two per SIMD): against four
