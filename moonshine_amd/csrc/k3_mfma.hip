@@ -380,8 +380,9 @@ struct TileCfg {
     static constexpr int OFF_A = 0, OFF_B = OFF_A + A_CH * 1024, STAGE = OFF_B + B_CH * 1024;
     static constexpr int OFF_SA = 0, OFF_SB = SA_CH * 1024, SBUF = (SA_CH + SB_CH) * 1024;
     static constexpr int LDS = STAGE * STAGES + 2 * SBUF;
-    /* two waves per SIMD (register-bound) read the second half of their A
-     * fragments after the first half's MFMAs */
+    /* eight waves (two per SIMD, register-bound) read A fragment q + 1
+     * under the MFMAs of fragment q; smaller blocks read all fragments
+     * in two halves */
     static constexpr bool SEQ = NWV > 4;
     static_assert(KS == 1 || KS == 2, "one or two K slices per stage");
     using DA = Deal<A_CH, NWV>;
@@ -623,13 +624,12 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
         bv[j] = ds_read16<(C::KS == 2 ? 2048 : 1024) * j>(b_base);
         sbw[j] = ds_read4<256 * j>(sb_base);
     });
-#ifndef K3_MFMA_NOPIPE
     if constexpr (C::SEQ) {
-        /* Software pipeline over the A fragments: the reads of fragment
-         * q + 1 are issued before the MFMAs of fragment q, so the LDS
-         * reads run under the matrix pipe instead of in a read phase
-         * with no MFMA in flight. Two fragment registers sets; LDS reads
-         * complete in order, so lgkmcnt(3) = all but fragment q + 1. */
+        /* Software pipeline over the A fragments (two waves per SIMD):
+         * the reads of fragment q + 1 are issued before the MFMAs of
+         * fragment q, so the LDS reads run under the matrix pipe instead
+         * of in a read phase with no MFMA in flight. LDS reads complete in
+         * order, so lgkmcnt(RA) = all but fragment q + 1. */
         read_a(std::integral_constant<int, 0>{});
         static_for<NA>([&](auto Q) {
             constexpr int q = decltype(Q)::value;
@@ -651,34 +651,6 @@ __device__ __forceinline__ void mfma_slice(f32x4 (&acc)[C::WM][C::WN], const uin
             mfmas(Q);
             __builtin_amdgcn_sched_barrier(0);
         });
-        return;
-    }
-#endif
-    if constexpr (C::SEQ) {
-        /* register-bound tiles: the second half's fragments are read into
-         * the registers the first half frees, after its MFMAs are issued */
-        static_for<H1>([&](auto I) { read_a(I); });
-        wait_lgkm<0>();
-        static_for<C::WN>([&](auto J) {
-            after_wait(bv[decltype(J)::value]);
-            after_wait(sbw[decltype(J)::value]);
-        });
-        static_for<H1>([&](auto I) {
-            after_wait(alo[decltype(I)::value]);
-            after_wait(ahi[decltype(I)::value]);
-            if constexpr (!C::AROW) after_wait(saw[decltype(I)::value]);
-        });
-        static_for<H1>([&](auto I) { mfmas(I); });
-        __builtin_amdgcn_sched_barrier(0);
-        static_for<H2>([&](auto I) { read_a(std::integral_constant<int, H1 + decltype(I)::value>{}); });
-        wait_lgkm<0>();
-        static_for<H2>([&](auto I) {
-            constexpr int q = H1 + decltype(I)::value;
-            after_wait(alo[q]);
-            after_wait(ahi[q]);
-            if constexpr (!C::AROW) after_wait(saw[q]);
-        });
-        static_for<H2>([&](auto I) { mfmas(std::integral_constant<int, H1 + decltype(I)::value>{}); });
         return;
     }
     static_for<H1>([&](auto I) { read_a(I); });
@@ -1159,11 +1131,8 @@ using Cls3 = TileCfg<2, 4, 4, 8, TERMS, 2>;
  * K step than a padded 128-row tile, 48 rows per wave. One term stages
  * 12 activation chunks, which do not split over 8 waves: it keeps the
  * 128-row blocks. */
-#ifndef K3_C2_AUX
-#define K3_C2_AUX 0
-#endif
 template <int TERMS>
-using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, K3_C2_AUX>, Cls3<TERMS>>;
+using Cls2 = std::conditional_t<TERMS == 2, TileCfg<2, 4, 3, 8, 2, 2, 1, 0>, Cls3<TERMS>>;
 
 /* LDS of a block running C or D: the ring and scale buffers are distinct
  * arrays (the pipeline names each buffer statically). */
