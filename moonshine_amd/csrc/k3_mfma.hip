@@ -1189,6 +1189,23 @@ __global__ __launch_bounds__(C::THREADS) void down_mfma_kernel(DownArgs A) {
     down_block<C>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
 }
 
+/* Three down classes of one block size in one launch (as gateup_mfma3_kernel;
+ * level with separate launches at cfg4, one launch where they are empty). */
+template <class C, class D, class E>
+__global__ __launch_bounds__(C::THREADS) void down_mfma3_kernel(DownArgs A, DownArgs B,
+                                                                DownArgs Ea, uint32_t na,
+                                                                uint32_t nb) {
+    static_assert(C::THREADS == D::THREADS && C::THREADS == E::THREADS, "one block size");
+    using R = RingSmem<C, D, E>;
+    K3_RING_SMEM(R);
+    if (blockIdx.x < na)
+        down_block<C>(A, blockIdx.x, b0, b1, b2, sbuf0, sbuf1);
+    else if (blockIdx.x < nb)
+        down_block<D>(B, blockIdx.x - na, b0, b1, b2, sbuf0, sbuf1);
+    else
+        down_block<E>(Ea, blockIdx.x - nb, b0, b1, b2, sbuf0, sbuf1);
+}
+
 
 template <class C>
 void launch_gateup(const GateUpArgs &a, uint32_t cap, hipStream_t st) {
@@ -1205,6 +1222,16 @@ template <class C>
 void launch_down(const DownArgs &a, uint32_t cap, hipStream_t st) {
     hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma_kernel<C>), dim3(xcd_grid(cap, a.H / C::BN)),
                        dim3(C::THREADS), 0, st, a);
+}
+
+template <class C, class D, class E>
+void launch_down3(const DownArgs &a, uint32_t cap_a, const DownArgs &b, uint32_t cap_b,
+                  const DownArgs &e, uint32_t cap_e, hipStream_t st) {
+    const uint32_t na = xcd_grid(cap_a, a.H / C::BN);
+    const uint32_t nb = na + xcd_grid(cap_b, b.H / D::BN);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(down_mfma3_kernel<C, D, E>),
+                       dim3(nb + xcd_grid(cap_e, e.H / E::BN)), dim3(C::THREADS), 0, st, a, b, e,
+                       na, nb);
 }
 
 template <class C, class D, class E>
@@ -1264,10 +1291,16 @@ bool launch_terms(const MfmaBuffers &B, uint16_t *y, const uint16_t *hidden,
         da.tiles = tl[c];
         da.tile_count = B.tile_count + c;
         if (c == 0) launch_down<Cls0<TERMS>>(da, B.tile_cap[c], st);
-        if (c == 1) launch_down<Cls1<TERMS>>(da, B.tile_cap[c], st);
-        /* (a paired launch measured level for down, whose blocks are short) */
-        if (c == 2) launch_down<Cls2<TERMS>>(da, B.tile_cap[c], st);
-        if (c == 3) launch_down<Cls3<TERMS>>(da, B.tile_cap[c], st);
+    }
+    if (B.tile_cap[3] || B.tile_cap[2] || B.tile_cap[1]) {
+        DownArgs d[kTileClasses];
+        for (int c = 1; c < kTileClasses; c++) {
+            d[c] = da;
+            d[c].tiles = tl[c];
+            d[c].tile_count = B.tile_count + c;
+        }
+        launch_down3<Cls3<TERMS>, Cls2<TERMS>, Cls1<TERMS>>(d[3], B.tile_cap[3], d[2],
+                                                            B.tile_cap[2], d[1], B.tile_cap[1], st);
     }
     return hipGetLastError() == hipSuccess;
 }
