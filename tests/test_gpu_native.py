@@ -60,6 +60,35 @@ def test_native_k3_decode_bitexact(cuda):
     np.testing.assert_array_equal(got, want["output"])
 
 
+@pytest.mark.timeout(600)
+def test_native_k3_mfma_batch_close_to_exact(cuda):
+    """The K3 layer at its real size (latent 3584: an odd count of 16-byte
+    scale records per gate/up weight row; F 3072), 64 tokens under the
+    MXFP8 precision against the exact precision of the same layer: the
+    same routes and weights, outputs within the MFMA bound."""
+    cfg = N.K3_NATIVE_LAYER
+    T = 64
+    layer = N.NativeLayer(cfg, device=cuda)
+    rng = np.random.default_rng(cfg.seed + T)
+    x = bf16_tensor(f32_to_bf16_bits(rng.normal(0, 1, (T, cfg.hidden)).astype(np.float32)), cuda)
+    r = bf16_tensor(f32_to_bf16_bits(rng.normal(0, 1, (T, cfg.hidden)).astype(np.float32)), cuda)
+    res = []
+    for precision in (0, 1):
+        ids = torch.zeros((T, cfg.top_k), dtype=torch.int32, device=cuda)
+        w = torch.zeros((T, cfg.top_k), dtype=torch.float32, device=cuda)
+        out = layer.forward(x, r, ids=ids, weights=w, precision=precision)
+        torch.cuda.synchronize()
+        res.append((bf16_bits(out), ids.cpu().numpy(), w.cpu().numpy()))
+    (ge, ie, we), (gm, im, wm) = res
+    np.testing.assert_array_equal(im, ie)
+    np.testing.assert_array_equal(wm, we)
+    gf = (gm.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    wf = (ge.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    rel = np.linalg.norm(gf - wf) / np.linalg.norm(wf)
+    print(f"\nK3-native T={T}: MFMA vs exact rel-L2 {rel:.3g}")
+    assert rel <= 2e-3, rel
+
+
 def test_native_mfma_close_to_exact(cuda):
     """MFMA expert products inside the native layer: routes stay exact; the
     output is within the MFMA precision's stated bound of the exact one."""
