@@ -276,3 +276,22 @@ def test_paired_class_launch_edges(cuda, T, k, rows):
     exact = moe.experts_only(x, ids_d, w_d, residual=r, precision=EXACT)
     torch.cuda.synchronize()
     assert_close(L.bf16_bits(out), L.bf16_bits(exact), f"paired classes {rows}")
+
+
+@pytest.mark.parametrize("T,H,F,E,k", [(33, 1024, 1024, 300, 2), (2, 3584, 1024, 300, 8),
+                                       (300, 1536, 1536, 64, 4), (100, 3584, 3072, 300, 8),
+                                       (257, 2560, 512, 8, 2), (180, 512, 3072, 16, 1)])
+def test_shapes_vs_exact(cuda, T, H, F, E, k):
+    """Shapes across the MFMA path's domain (hidden, ffn % 512; odd and even
+    scale-record counts; top-k 1..8; 2 to 300 tokens; few experts, so
+    every tile class fills): MFMA against the exact path, routes
+    identical."""
+    cfg = dataclasses.replace(CONFIGS[0], name=f"s{T}x{H}x{F}x{E}x{k}", tokens=T, hidden=H, ffn=F,
+                              experts=E, top_k=k, seed=800 + T + E)
+    inputs = make_inputs(cfg, tokens=T)
+    moe = get_layer(cfg, inputs, cuda)
+    out, ids, w = forward(moe, inputs, cuda, MFMA)
+    exact, ids_e, w_e = forward(moe, inputs, cuda, EXACT)
+    np.testing.assert_array_equal(ids, ids_e)
+    np.testing.assert_array_equal(w, w_e)
+    assert_close(out, exact, f"{cfg.name} mfma vs exact")
