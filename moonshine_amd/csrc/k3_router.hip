@@ -14,6 +14,8 @@
  *                          approximate logits and a rigorous error bound,
  *                          exact w64-order logits for the candidates only,
  *                          then the exact router's top-k on exact keys
+ *   router_certify_wave_kernel  the same with one wave per token, for
+ *                          batches of 1024 tokens and more
  *
  * Why the routes are exact. Let p_i = w_i x_i (exact in fp32: bf16 x bf16
  * products have 16 significant bits), u = 2^-24. Each MFMA instruction sums
@@ -31,16 +33,18 @@
  * The choice is sigmoid(l) + bias. The real sigmoid's slope on [a - err,
  * a + err] is at most s'(max(0, |a| - err)) (the slope falls away from 0),
  * the router sigmoid (router_sigmoid, the hardware exp2/reciprocal sequence)
- * is within 3e-7 of the real one and the bias add rounds once, so the approximate and exact choices differ by at most
- * ce_e = s'(..) err_e + 2e-6 + 2^-21 |c_e|. If T_k is the k-th largest
- * approximate choice and E_k the largest ce among the experts at or above
- * it, those k experts have exact choices >= T_k - E_k, so every expert of
- * the exact top-k (ties included) has approximate choice + ce_e >= T_k -
- * E_k. Those are the candidates; every other expert gets key 0 (never
- * selected) and the candidates get their exact keys, so topk_select_wave
- * returns what it returns on all exact keys. A token with any non-finite
- * input, approximate logit, norm or bias takes every expert as a candidate
- * (the exact router on that token).
+ * is within 3e-7 of the real one and the bias add rounds once, so the
+ * approximate and exact choices differ by at most ce_e = s'(..) err_e + 2e-6
+ * + 2^-21 |c_e|, with s'(m) bounded from above by sigmoid_slope_bound.
+ * If T_k is the k-th largest approximate choice and E_k the largest ce
+ * among the experts at or above it, those k experts have exact choices >=
+ * T_k - E_k, so every expert of the exact top-k (ties included) has
+ * approximate choice + ce_e >= T_k - E_k. Those are the candidates; every
+ * other expert gets key 0 (never selected) and the candidates get their
+ * exact keys, so the selection returns what it returns on all exact keys.
+ * A token with any non-finite input, approximate logit, norm or bias, or
+ * an error bound above 1e30, takes every expert as a candidate (the exact
+ * router on that token).
  */
 #include "k3_decode.h"
 #include "k3_device.h"
@@ -283,6 +287,24 @@ __device__ __forceinline__ float key_value(uint32_t key) {
 
 constexpr uint32_t kNanBits = 0x7fc00000u;
 
+/* batches of at least this many tokens certify with one wave per token
+ * (cfg4, 8192 tokens: 365 -> 191 us; at 64 and 512 tokens the block per
+ * token is faster: 34 vs 41 us, 39 vs 43 us) */
+constexpr uint32_t kCertWaveMinTokens = 1024;
+
+/* Slope bound of the real sigmoid at m >= 0: s(m) (1 - s(m)) = e / (1 +
+ * e)^2 with e = exp(-m), formed from e with the hardware exp2 and
+ * reciprocal (each within 1 ulp) and products only, so every step is
+ * accurate to a small relative error (the argument's rounding moves 2^t
+ * by < 2^-16 relative for m < 88) and 1 - s never cancels; the factor 1 +
+ * 2^-10 covers all of it. 0 for m >= 88 (the real slope is below 2^-126
+ * there; callers take tokens with err > 1e30 down the exact path). */
+__device__ __forceinline__ float sigmoid_slope_bound(float m) {
+    const float e = __builtin_amdgcn_exp2f(__fmul_rn(fminf(m, 88.0f), -1.44269502162933349609375f));
+    const float r = __builtin_amdgcn_rcpf(__fadd_rn(1.0f, e));
+    return __fmul_rn(__fmul_rn(__fmul_rn(e, r), r), 1.0f + 1.0f / 1024.0f);
+}
+
 /* Scratch of one certify block (one token). */
 struct CertSmem {
     uint4 x[64 * kTopkSlots];       /* the token's row, 8-element chunks */
@@ -354,10 +376,9 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
                 ch[j] = __fadd_rn(s, bs[j]);
                 const float err = fmaf(__fmul_rn(A.err_coef, nb[j]), nx, 1e-30f);
                 const float m = fmaxf(0.0f, __fsub_rn(fabsf(la[j]), err));
-                const float sm_ = det_sigmoid(m);
-                const float slope = __fmul_rn(__fmul_rn(sm_, __fsub_rn(1.0f, sm_)),
-                                              1.0f + 1.0f / 1024.0f);
-                ce[j] = fmaf(slope, err, fmaf(4.76837158203125e-7f, fabsf(ch[j]), 2e-6f));
+                fin = fin && err <= 1e30f;
+                ce[j] = fmaf(sigmoid_slope_bound(m), err,
+                             fmaf(4.76837158203125e-7f, fabsf(ch[j]), 2e-6f));
             }
         }
         /* the k-th largest approximate key */
@@ -469,6 +490,249 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
                      A.ids2 ? A.ids2 + o : nullptr, A.w2 ? A.w2 + o : nullptr, sm.topk);
 }
 
+/* The k-th largest (with multiplicity) of the wave's keys, key[j] of lane l
+ * for expert l + 64 j; 0 when fewer than k keys are nonzero. The k-th
+ * largest lane maximum M is a lower bound (the k lanes with the largest
+ * maxima hold k keys >= M), so only the keys >= M -- a few dozen -- are
+ * ranked, one per lane from `scratch` (64 words); more than 64 of them
+ * (heavy ties) take a 32-step bitwise search over every key. */
+__device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[kTopkSlots], uint32_t k,
+                                                    uint32_t *scratch) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t lmax = 0u;
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) lmax = key[j] > lmax ? key[j] : lmax;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t t = m | (1u << b);
+        if ((uint32_t)__popcll(__ballot(lmax >= t)) >= k) m = t;
+    }
+    uint32_t mine = 0u;
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) mine += (m != 0u && key[j] >= m) ? 1u : 0u;
+    const uint32_t total = wave_count(mine);
+    if (m != 0u && total <= 64u) {
+        const unsigned long long below = (1ull << lane) - 1ull;
+        uint32_t pos = 0u;
+#pragma unroll
+        for (int b = 0; b < 5; b++)
+            pos += (uint32_t)__popcll(__ballot((mine >> b) & 1u) & below) << b;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++)
+            if (key[j] >= m) scratch[pos++] = key[j];
+        wave_fence();
+        const uint32_t ck = lane < total ? scratch[lane] : 0u;
+        uint32_t gt = 0u, ge = 0u;
+        for (uint32_t i = 0; i < total; i++) {
+            const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)i);
+            gt += o > ck ? 1u : 0u;
+            ge += o >= ck ? 1u : 0u;
+        }
+        wave_fence(); /* scratch is reused by the caller */
+        const unsigned long long hit = __ballot(lane < total && gt < k && k <= ge);
+        return (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)(__ffsll((long long)hit) - 1));
+    }
+    uint32_t thr = 0u;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t tt = thr | (1u << b);
+        uint32_t cnt = 0u;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) cnt += key[j] >= tt ? 1u : 0u;
+        if (wave_count(cnt) >= k) thr = tt;
+    }
+    return thr;
+}
+
+/*
+ * The certification of router_certify_kernel with one wave per token (4
+ * tokens per block, no block barriers), for large batches: the phases a
+ * block runs with one busy wave (candidate list, selection) no longer
+ * idle three others, and twice as many tokens are in flight per CU. The
+ * token's row stays in registers (lane l holds chunks l, l + 64, ..., the
+ * w64 order's), the candidate rows are computed two in flight, and the
+ * selection runs on the candidates only:
+ *   candidates  approximate keys, T_k by kth_largest_key, E_k, the bound
+ *               lim; candidate ids and biases go to the wave's
+ *               cand_id / cand_score (positions in expert order);
+ *   exact       w64-order logits of the candidates (into cand_key);
+ *   select      each candidate's exact key (router_sigmoid + bias) and
+ *               weight score (det_sigmoid), compacted to keys != 0, then
+ *               topk_rank_write: the exact router's ranking and weights.
+ * Same bound, same candidates' keys and the same ranking as the block
+ * kernel, so the same routes.
+ */
+__global__ __launch_bounds__(256, 2) void router_certify_wave_kernel(CertArgs A) {
+    __shared__ TopkWaveSmem smem[4];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = 4u * blockIdx.x + wave;
+    if (t >= A.T) return; /* wave-uniform; the waves share no barrier */
+    TopkWaveSmem &sm = smem[wave];
+    const uint32_t E = A.E, H = A.H, chunks = H / 8u;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    /* one batch of loads: the row's chunks, approximate logits, norms,
+     * biases */
+    const uint4 *xr = (const uint4 *)(A.x + (uint64_t)t * H);
+    const float *ar = A.approx + (uint64_t)t * E;
+    float la[kTopkSlots], nb[kTopkSlots], bs[kTopkSlots];
+    float ss = 0.0f;
+    {
+        /* the row for its norm only: it is read again (from L2) for the
+         * exact logits rather than held through the candidate phase */
+        uint4 xn[kTopkSlots];
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t c = lane + 64u * (uint32_t)j, e = c;
+            xn[j] = c < chunks ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+            la[j] = e < E ? ar[e] : 0.0f;
+            nb[j] = e < E ? A.norms[e] : 0.0f;
+            bs[j] = e < E ? A.bias[e] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t u[4] = {xn[j].x, xn[j].y, xn[j].z, xn[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                ss = fmaf(bf16_lo(u[q]), bf16_lo(u[q]), ss);
+                ss = fmaf(bf16_hi(u[q]), bf16_hi(u[q]), ss);
+            }
+        }
+    }
+    const float nx = __fmul_rn(__fsqrt_rn(wave_sum(ss)), kNormInflate);
+    bool fin = isfinite(nx);
+    uint32_t key[kTopkSlots];
+    float ch[kTopkSlots], ce[kTopkSlots];
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) {
+        const uint32_t e = lane + 64u * (uint32_t)j;
+        key[j] = 0u;
+        ch[j] = 0.0f;
+        ce[j] = 0.0f;
+        if (e < E) {
+            fin = fin && isfinite(la[j]) && isfinite(nb[j]) && isfinite(bs[j]);
+            const float s = router_sigmoid(la[j]);
+            key[j] = choice_key(s, bs[j]);
+            ch[j] = __fadd_rn(s, bs[j]);
+            const float err = fmaf(__fmul_rn(A.err_coef, nb[j]), nx, 1e-30f);
+            fin = fin && err <= 1e30f;
+            const float m = fmaxf(0.0f, __fsub_rn(fabsf(la[j]), err));
+            ce[j] = fmaf(sigmoid_slope_bound(m), err,
+                         fmaf(4.76837158203125e-7f, fabsf(ch[j]), 2e-6f));
+        }
+    }
+    const bool exact_all = __ballot(!fin) != 0ull;
+    uint32_t thr = exact_all ? 0u : kth_largest_key(key, A.k, sm.cand_key);
+    float lim = 0.0f;
+    const bool every = exact_all || thr == 0u;
+    if (!every) {
+        float ek = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++)
+            if (key[j] >= thr) ek = fmaxf(ek, ce[j]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ek = fmaxf(ek, __shfl_xor(ek, o, 64));
+        lim = __fsub_rn(key_value(thr), ek);
+        lim = __fsub_rn(lim, __fmul_rn(fabsf(lim), 2.384185791015625e-7f));
+    }
+    uint32_t mine = 0u;
+    bool cand[kTopkSlots];
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) {
+        const uint32_t e = lane + 64u * (uint32_t)j;
+        cand[j] = e < E && (every || __fadd_rn(ch[j], ce[j]) >= lim);
+        mine += cand[j] ? 1u : 0u;
+    }
+    uint32_t pos = 0u, ncand = 0u;
+#pragma unroll
+    for (int b = 0; b < 5; b++) {
+        const unsigned long long m = __ballot((mine >> b) & 1u);
+        pos += (uint32_t)__popcll(m & below) << b;
+        ncand += (uint32_t)__popcll(m) << b;
+    }
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) {
+        if (cand[j]) {
+            sm.cand_id[pos] = lane + 64u * (uint32_t)j;
+            sm.cand_score[pos] = bs[j]; /* the bias until the selection */
+            pos++;
+        }
+    }
+    wave_fence();
+    uint4 xv[kTopkSlots];
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) {
+        const uint32_t c = lane + 64u * (uint32_t)j;
+        xv[j] = c < chunks ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    /* exact w64-order logits, two candidate rows in flight */
+    auto load_row = [&](uint32_t p, uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) {
+        const uint32_t eu = (uint32_t)__builtin_amdgcn_readfirstlane((int)sm.cand_id[p]);
+        const uint4 *wr = (const uint4 *)(A.w + (uint64_t)eu * H);
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            const uint32_t c = lane + 64u * (uint32_t)j;
+            v[j] = wr[c < chunks ? c : chunks - 1u];
+        }
+    };
+    auto dot_row = [&](const uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) -> float {
+        float s1[1] = {0.0f};
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) {
+            if (lane + 64u * (uint32_t)j < chunks) {
+                /* opaque copy: keeps the row's fp32 conversions inside the
+                 * loop over candidates (hoisted, they would take 128
+                 * registers) */
+                uint32_t xu[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+                asm volatile("" : "+v"(xu[0]), "+v"(xu[1]), "+v"(xu[2]), "+v"(xu[3]));
+                const uint32_t a[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    s1[0] = fmaf(bf16_lo(a[q]), bf16_lo(xu[q]), s1[0]);
+                    s1[0] = fmaf(bf16_hi(a[q]), bf16_hi(xu[q]), s1[0]);
+                }
+            }
+        }
+        return wave_sum_rows<1>(s1);
+    };
+    uint4 wa[kTopkSlots], wb[kTopkSlots];
+    if (ncand > 0u) load_row(0u, wa);
+    for (uint32_t p = 0; p < ncand; p += 2u) {
+        const bool second = p + 1u < ncand;
+        if (second) load_row(p + 1u, wb);
+        const float l1 = dot_row(wa);
+        if (lane == 0u) sm.cand_key[p] = __float_as_uint(l1);
+        if (!second) break;
+        if (p + 2u < ncand) load_row(p + 2u, wa);
+        const float l2 = dot_row(wb);
+        if (lane == 0u) sm.cand_key[p + 1u] = __float_as_uint(l2);
+    }
+    wave_fence();
+    /* exact keys and weight scores of the candidates, compacted to keys
+     * != 0 (a NaN choice is never selected) */
+    uint32_t nlive = 0u;
+    for (uint32_t base = 0; base < ncand; base += 64u) {
+        const uint32_t p = base + lane;
+        const bool live = p < ncand;
+        const float l = live ? __uint_as_float(sm.cand_key[p]) : 0.0f;
+        const uint32_t e = live ? sm.cand_id[p] : 0u;
+        const float b = live ? sm.cand_score[p] : 0.0f;
+        const uint32_t kk = live ? choice_key(router_sigmoid(l), b) : 0u;
+        const float sc = det_sigmoid(l);
+        const unsigned long long okm = __ballot(kk != 0u);
+        const uint32_t q = nlive + (uint32_t)__popcll(okm & below);
+        if (kk != 0u) {
+            sm.cand_key[q] = kk;
+            sm.cand_id[q] = e;
+            sm.cand_score[q] = sc;
+        }
+        nlive += (uint32_t)__popcll(okm);
+    }
+    wave_fence();
+    const uint64_t o = (uint64_t)t * A.k;
+    topk_rank_write(nlive, A.k, A.scale, A.ids + o, A.weights + o, A.ids2 ? A.ids2 + o : nullptr,
+                    A.w2 ? A.w2 + o : nullptr, sm, TopkNoHooks{});
+}
+
 }  // namespace
 
 /* K slices of the MFMA logits: enough (tile, slice) works to spread over
@@ -533,7 +797,10 @@ bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, floa
     CertArgs A{ids, weights, ids2, w2, approx, norms, (const float *)router_bias,
                (const uint16_t *)x, w, T, E, H, k, scale,
                (float)(H / 32u + 270u) * 5.9604644775390625e-8f * (1.0f + 1.0f / 1024.0f)};
-    hipLaunchKernelGGL(router_certify_kernel, dim3(T), dim3(256), 0, st, A);
+    if (T >= kCertWaveMinTokens)
+        hipLaunchKernelGGL(router_certify_wave_kernel, dim3((T + 3u) / 4u), dim3(256), 0, st, A);
+    else
+        hipLaunchKernelGGL(router_certify_kernel, dim3(T), dim3(256), 0, st, A);
     return hipGetLastError() == hipSuccess;
 }
 

@@ -79,6 +79,12 @@ __device__ __forceinline__ uint32_t topk_rank_lanes(uint32_t mk, uint32_t mi, ui
     return cnt;
 }
 
+template <class Hooks>
+__device__ __forceinline__ uint32_t topk_rank_write(uint32_t ncand, uint32_t top_k, float scale,
+                                                    uint32_t *ids, float *weights,
+                                                    uint32_t *ids_copy, float *w_copy,
+                                                    TopkWaveSmem &sm, Hooks &&hooks);
+
 /* key[j]/score[j] for expert lane + 64 j. Writes ids/weights[0..top_k) (and
  * the optional copies, which may be host-mapped). Must be called by all 64
  * lanes of the wave; 1 <= top_k <= 32. Returns the rank-`lane` id to lanes
@@ -125,6 +131,19 @@ __device__ __forceinline__ uint32_t topk_select_wave(const uint32_t (&key)[kTopk
         }
     }
     wave_fence();
+    return topk_rank_write(ncand, top_k, scale, ids, weights, ids_copy, w_copy, sm, hooks);
+}
+
+/* Second half of topk_select_wave: ranks the ncand candidates in
+ * sm.cand_key / cand_id / cand_score (keys >= 1) by (key desc, id asc) and
+ * writes the first top_k as topk_select_wave does. Must be called by all
+ * 64 lanes after the candidates' LDS writes have completed. */
+template <class Hooks>
+__device__ __forceinline__ uint32_t topk_rank_write(uint32_t ncand, uint32_t top_k, float scale,
+                                                    uint32_t *ids, float *weights,
+                                                    uint32_t *ids_copy, float *w_copy,
+                                                    TopkWaveSmem &sm, Hooks &&hooks) {
+    const uint32_t lane = threadIdx.x & 63u;
     if (ncand <= 64u) {
         const bool live = lane < ncand;
         const uint32_t mk = live ? sm.cand_key[lane] : 0u, mi = live ? sm.cand_id[lane] : 0u;

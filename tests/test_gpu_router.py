@@ -82,7 +82,8 @@ def test_certified_router_k3_prefill(cuda):
 @pytest.mark.parametrize("T,E,H,k", [(128, 64, 512, 4), (300, 200, 1024, 8), (517, 896, 7168, 16),
                                      (1000, 1024, 8192, 32), (130, 40, 64, 1), (33, 896, 7168, 16),
                                      (64, 256, 2048, 8), (31, 64, 512, 4), (129, 896, 7168, 16),
-                                     (257, 1000, 1024, 8)])
+                                     (257, 1000, 1024, 8), (1024, 896, 7168, 16),
+                                     (1500, 300, 1024, 8), (2048, 64, 512, 32)])
 def test_certified_router_shapes(cuda, T, E, H, k):
     rng = np.random.default_rng(T * 7 + E)
     w = bf16(rng.normal(0, 0.02, (E, H)))
@@ -91,12 +92,15 @@ def test_certified_router_shapes(cuda, T, E, H, k):
     check(w, b, x, k, 2.5, cuda, bound_rows=np.arange(T))
 
 
-def test_certified_router_adversarial(cuda):
+@pytest.mark.parametrize("T", [256, 1100])
+def test_certified_router_adversarial(cuda, T):
     """Exact logit ties (duplicated router rows, equal biases), all-zero
     tokens (every choice equal), huge, tiny and non-finite tokens, and a
-    bias that dominates the logits."""
+    bias that dominates the logits; at 1100 tokens (one wave per token)
+    also one bias for every expert, so the all-zero token's 256 keys tie
+    (more than 64 at the threshold: the full bitwise search)."""
     rng = np.random.default_rng(5)
-    T, E, H, k = 256, 256, 1024, 8
+    E, H, k = 256, 1024, 8
     wf = rng.normal(0, 0.02, (E, H)).astype(np.float32)
     wf[1::2] = wf[0::2]  # rows 2j and 2j + 1 equal
     w = bf16(wf)
@@ -116,6 +120,8 @@ def test_certified_router_adversarial(cuda):
     assert (ids[9:] >= 0).all()
     big_bias = rng.normal(0, 10.0, E).astype(np.float32)
     check(w, big_bias, x, k, 1.0, cuda)
+    if T > 1000:
+        check(w, np.full(E, 0.25, np.float32), x, k, 1.0, cuda)
 
 
 def test_router_sigmoid_exhaustive_bound(cuda):

@@ -13,8 +13,9 @@
    above it, the exact top-k (ties towards the lower id) satisfies
    c~ + ce >= T_k - E_k. Brute force over random and adversarial cases
    (errors pushed to the bound against the true order, exact ties), with
-   the slope and ce formed in fp32 in the kernel's order from the
-   deterministic sigmoid the kernel uses for the slope.
+   the slope and ce formed in fp32 in the kernel's order
+   (sigmoid_slope_bound: e = 2^(-m log2 e), slope = e / (1 + e)^2, every
+   step relative-accurate).
 """
 import numpy as np
 
@@ -53,12 +54,15 @@ def det_sigmoid_f32(z, rng):
 def candidates(a, err, bias, k, rng):
     s = det_sigmoid_f32(a, rng)
     ch = (s + bias).astype(np.float32)
-    # the kernel's fp32 sequence: m = max(0, |a| - err); sm = det_sigmoid(m);
-    # slope = (sm * (1 - sm)) * (1 + 2^-10); ce = fma(slope, err, fma(2^-21, |c|, 2e-6))
+    # the kernel's fp32 sequence (sigmoid_slope_bound): m = max(0, |a| - err);
+    # e = 2^(min(m, 88) * -log2 e); r = 1 / (1 + e); slope = ((e r) r) (1 + 2^-10);
+    # ce = fma(slope, err, fma(2^-21, |c|, 2e-6))
     m = np.maximum(np.float32(0), (np.abs(a) - err).astype(np.float32)).astype(np.float32)
-    sm = np.array([L.k3o_sigmoid(float(v), 0) for v in m], np.float32)
-    slope = ((sm * (np.float32(1) - sm)).astype(np.float32) *
-             np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
+    tt = (np.minimum(m, np.float32(88)) * np.float32(-1.44269502162933349609375)).astype(np.float32)
+    e = np.exp2(tt.astype(np.float64)).astype(np.float32)
+    r = (1.0 / (np.float64(1) + e).astype(np.float32).astype(np.float64)).astype(np.float32)
+    slope = ((e * r).astype(np.float32) * r).astype(np.float32)
+    slope = (slope * np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
     ce = np.array([fmaf(slope[i], err[i], fmaf(4.76837158203125e-7, abs(ch[i]), 2e-6))
                    for i in range(len(ch))], np.float32)
     order = np.lexsort((np.arange(len(ch)), -ch.astype(np.float64)))
@@ -107,3 +111,22 @@ def test_candidate_rule_keeps_exact_topk():
         want = exact_topk(l, bias, k, rng)
         assert cand[want].all(), (trial, E, k)
         assert cand.sum() >= k
+
+
+def test_slope_bound_covers_the_sigmoid_slope():
+    """The kernel's slope (sigmoid_slope_bound: e = 2^(-m log2 e), slope =
+    ((e r) r)(1 + 2^-10), r = 1 / (1 + e)) is at least the real slope
+    s(m)(1 - s(m)) over [0, 88), with 4 ulp of slack for the hardware exp2
+    and reciprocal (each within 1 ulp), and the real slope is below 2^-126
+    past 88, where the kernel returns 0."""
+    m = np.concatenate([np.linspace(0, 88, 2_000_001), np.geomspace(1e-8, 88, 200_001)])
+    m = m.astype(np.float32)
+    tt = (np.minimum(m, np.float32(88)) * np.float32(-1.44269502162933349609375)).astype(np.float32)
+    e = np.exp2(tt.astype(np.float64)).astype(np.float32)
+    r = (1.0 / (np.float64(1) + e).astype(np.float32).astype(np.float64)).astype(np.float32)
+    slope = ((e * r).astype(np.float32) * r).astype(np.float32)
+    slope = (slope * np.float32(1.0 + 2.0 ** -10)).astype(np.float64)
+    md = m.astype(np.float64)
+    real = np.exp(-md) / (1.0 + np.exp(-md)) ** 2
+    assert (slope * (1.0 - 4 * 2.0 ** -23) >= real).all()
+    assert np.exp(-88.0) < 2.0 ** -126
