@@ -49,6 +49,7 @@
 #include "k3_decode.h"
 #include "k3_device.h"
 #include "k3_internal.h"
+#include "k3_lds.h"
 #include "k3_topk.h"
 
 #include <hip/hip_runtime.h>
@@ -97,75 +98,47 @@ __global__ __launch_bounds__(256) void router_norms_kernel(float *__restrict__ n
 /*
  * out[t, e] ~= x_t . w_e, summed as described above (C = 0 MFMAs, fp32
  * adds of the 32-product blocks). Block tile 128 tokens x 128 experts, 8
- * waves of 32 x 64 (2 x 4 V_MFMA_F32_16X16X32_BF16 tiles), K steps of 64
- * staged in two LDS buffers (rows padded to 144 bytes so the 16 rows of a fragment
- * read fall on different banks). Lane l = 16 g + c supplies row c of a
- * fragment with the 8 bf16 at K offset 8 g (A: tokens, B: experts; the
- * same K assignment on both operands, which is all a dot product needs);
- * it receives tokens 4 g .. 4 g + 3 of expert column c. Rows past T or E
- * load the last valid row and are not stored. Tiles are dealt to the XCDs
- * in contiguous ranges, a token tile's expert tiles together, so one XCD's
- * L2 serves a token tile to all of its expert tiles.
+ * waves of 32 x 64 (2 x 4 V_MFMA_F32_16X16X32_BF16 tiles), two blocks per
+ * CU, K steps of 64 (one 128-byte line per row) staged by direct-to-LDS
+ * loads in two buffers: 16 KB of token rows and 16 KB of expert rows per
+ * step, eight whole lines per 1 KB chunk with the XOR swizzle of a_slot,
+ * so the 16 lanes of each fragment read pass fall on 16 different 16-byte
+ * bank groups. Lane l = 16 g + c supplies row c of a fragment with the 8
+ * bf16 at K offset 8 g (A: tokens, B: experts; the same K assignment on
+ * both operands, which is all a dot product needs); it receives tokens 4 g
+ * .. 4 g + 3 of expert column c. Rows past T or E load the last valid row
+ * and are not stored. Tiles are dealt to the XCDs in contiguous ranges, a
+ * token tile's expert tiles together, so one XCD's L2 serves a token tile
+ * to all of its expert tiles. Measured at cfg4 (8192 x 896 x 7168): 0.15
+ * ms; staging through registers ran at ~16 bytes per clock per CU (0.23
+ * ms), and 128 x 224 tiles with three buffers and one block per CU (one
+ * tile per CU) at 0.17 ms.
  */
-constexpr uint32_t kRT = 128, kRK = 64, kRPad = 144;
+constexpr uint32_t kRT = 128, kRK = 64;
+constexpr uint32_t kRStage = 2u * kRT * 128u; /* [token rows | expert rows] */
 
-typedef uint8_t RouterStage[2][kRT * kRPad]; /* [A tokens | B experts] rows */
-
-__device__ __forceinline__ void rt_load(uint4 &a0, uint4 &a1, uint4 &b0, uint4 &b1,
-                                        const uint8_t *xb, const uint8_t *wb,
-                                        const uint32_t (&ao)[2], const uint32_t (&bo)[2],
-                                        uint32_t kb) {
-    /* byte offsets of the thread's two rows (< 2^31: T H 2 bytes) */
-    a0 = *(const uint4 *)(xb + ao[0] + kb);
-    a1 = *(const uint4 *)(xb + ao[1] + kb);
-    b0 = *(const uint4 *)(wb + bo[0] + kb);
-    b1 = *(const uint4 *)(wb + bo[1] + kb);
-}
-
-__device__ __forceinline__ void rt_store(RouterStage &buf, uint32_t off, const uint4 &a0,
-                                         const uint4 &a1, const uint4 &b0, const uint4 &b1) {
-    constexpr uint32_t R64 = 64u * kRPad;
-    *(uint4 *)(buf[0] + off) = a0;
-    *(uint4 *)(buf[0] + off + R64) = a1;
-    *(uint4 *)(buf[1] + off) = b0;
-    *(uint4 *)(buf[1] + off + R64) = b1;
-}
-
-__device__ __forceinline__ void rt_compute(f32x4_t (&acc)[2][4], const RouterStage &buf,
-                                           uint32_t a_off, uint32_t b_off) {
+/* Step loads of one wave into `stage`: chunks wave and wave + 8 of each
+ * region (chunk q holds rows 16 (q / 2) + 8 (q % 2) + lane / 8); src[] are
+ * the lane's byte offsets (token rows, then expert rows), kb the step's K
+ * byte offset. */
+__device__ __forceinline__ void rt_issue(uint8_t *stage, const uint8_t *xb, const uint8_t *wb,
+                                         const uint32_t (&src)[4], uint32_t kb, uint32_t wave) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-        bf16x8_t af[2], bf[4];
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            af[i] = __builtin_bit_cast(bf16x8_t, *(const uint4 *)(buf[0] + a_off + 16u * kRPad * i +
-                                                                  64u * ks));
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            bf[j] = __builtin_bit_cast(bf16x8_t, *(const uint4 *)(buf[1] + b_off + 16u * kRPad * j +
-                                                                  64u * ks));
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                /* a fresh 32-term dot product per instruction (C = 0),
-                 * accumulated with one fp32 add per K block */
-                const f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    af[i], bf[j], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[i][j][r] = __fadd_rn(acc[i][j][r], d[r]);
-            }
+    for (int u = 0; u < 2; u++) {
+        const uint32_t q = wave + 8u * (uint32_t)u;
+        dma<16>(xb + src[u] + kb, stage + 1024u * q);
+        dma<16>(wb + src[2 + u] + kb, stage + kRT * 128u + 1024u * q);
     }
 }
 
 /* 8 waves: wave w covers tokens 32 (w / 2) .. + 32 and experts 64 (w % 2)
  * .. + 64 of the block's 128 x 128 tile. */
-__global__ __launch_bounds__(512) void router_mfma_kernel(float *__restrict__ out,
-                                                          const uint16_t *__restrict__ x,
-                                                          const uint16_t *__restrict__ w,
-                                                          uint32_t T, uint32_t E, uint32_t H,
-                                                          uint32_t S) {
-    __shared__ __attribute__((aligned(16))) RouterStage lds[2];
+__global__ __launch_bounds__(512, 4) void router_mfma_kernel(float *__restrict__ out,
+                                                             const uint16_t *__restrict__ x,
+                                                             const uint16_t *__restrict__ w,
+                                                             uint32_t T, uint32_t E, uint32_t H,
+                                                             uint32_t S) {
+    __shared__ __attribute__((aligned(16))) uint8_t st0[kRStage], st1[kRStage];
     const uint32_t ntt = (T + kRT - 1u) / kRT, net = (E + kRT - 1u) / kRT;
     const uint32_t works = ntt * net * S, per = (works + 7u) / 8u;
     const uint32_t L = blockIdx.x, j8 = L >> 3, wk0 = (L & 7u) * per + j8;
@@ -176,21 +149,19 @@ __global__ __launch_bounds__(512) void router_mfma_kernel(float *__restrict__ ou
     out += (uint64_t)slice * T * E;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1u, g = lane >> 4, c = lane & 15u;
-    /* thread tid loads 16-byte piece tid % 8 of rows tid / 8 and tid / 8 +
-     * 64; rows past T or E clamp to the last one (their results are not
-     * stored) */
-    const uint32_t r0 = tid >> 3, pc = tid & 7u;
-    uint32_t ao[2], bo[2];
+    /* the lane's source byte offsets: chunk q = wave + 8 u holds rows 16 (q
+     * / 2) + a_dma_row(lane, q % 2), piece a_dma_piece(lane, q % 2); rows
+     * past T or E clamp to the last one (their results are not stored) */
+    uint32_t src[4];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t ta = t0 + r0 + 64u * i, eb = e0 + r0 + 64u * i;
-        ao[i] = ((ta < T ? ta : T - 1u) * H + 8u * pc) * 2u;
-        bo[i] = ((eb < E ? eb : E - 1u) * H + 8u * pc) * 2u;
+    for (int u = 0; u < 2; u++) {
+        const uint32_t q = wave + 8u * (uint32_t)u, h = q & 1u;
+        const uint32_t r = 16u * (q >> 1) + a_dma_row(lane, h), pc = a_dma_piece(lane, h);
+        const uint32_t ta = t0 + r, eb = e0 + r;
+        src[u] = ((ta < T ? ta : T - 1u) * H + 8u * pc) * 2u;
+        src[2 + u] = ((eb < E ? eb : E - 1u) * H + 8u * pc) * 2u;
     }
     const uint8_t *xb = (const uint8_t *)x, *wb = (const uint8_t *)w;
-    const uint32_t soff = r0 * kRPad + 16u * pc;
-    const uint32_t a_off = (32u * wm + c) * kRPad + 16u * g;
-    const uint32_t b_off = (64u * wn + c) * kRPad + 16u * g;
     f32x4_t acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -199,30 +170,56 @@ __global__ __launch_bounds__(512) void router_mfma_kernel(float *__restrict__ ou
     /* this slice's K steps [s0, s0 + nsteps) */
     const uint32_t ksteps = H / kRK;
     const uint32_t s0 = ksteps * slice / S, nsteps = ksteps * (slice + 1u) / S - s0;
-    const uint32_t last = nsteps - 1u;
     xb += 2u * kRK * s0;
     wb += 2u * kRK * s0;
-    /* two register sets: step s + 2's loads are issued at the start of
-     * step s, so each load has two steps of MFMAs to land. Loads and
-     * stores are unconditional (steps past the end reload the last one
-     * into a buffer nobody reads). */
-    uint4 a0, a1, b0, b1, p0, p1, q0, q1;
-    rt_load(a0, a1, b0, b1, xb, wb, ao, bo, 0u);
-    rt_load(p0, p1, q0, q1, xb, wb, ao, bo, 2u * kRK * (1u < last ? 1u : last));
-    rt_store(lds[0], soff, a0, a1, b0, b1);
-    __syncthreads();
+    /* fragment addresses: A rows 32 wm + 16 i + c, B rows 64 wn + 16 j + c
+     * (chunk pair = 16 rows = 2 KB) */
+    auto step = [&](const uint8_t *cur) __attribute__((always_inline)) {
+        const uint32_t base = lds_addr(cur);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const uint32_t a0 = base + 2048u * (2u * wm) + a_slot(c, 4u * (uint32_t)ks + g);
+            const uint32_t b0 = base + kRT * 128u + 2048u * (4u * wn) + a_slot(c, 4u * (uint32_t)ks + g);
+            u32x4_t af[2], bf[4];
+            af[0] = ds_read16<0>(a0);
+            af[1] = ds_read16<2048>(a0);
+            bf[0] = ds_read16<0>(b0);
+            bf[1] = ds_read16<2048>(b0);
+            bf[2] = ds_read16<4096>(b0);
+            bf[3] = ds_read16<6144>(b0);
+            wait_lgkm<0>();
+#pragma unroll
+            for (int i = 0; i < 2; i++) after_wait(af[i]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) after_wait(bf[j]);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    /* a fresh 32-term dot product per instruction (C = 0),
+                     * accumulated with one fp32 add per K block */
+                    const f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8_t, af[i]), __builtin_bit_cast(bf16x8_t, bf[j]),
+                        f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] = __fadd_rn(acc[i][j][r], d[r]);
+                }
+        }
+    };
+    /* step s: wait for this wave's loads of s, barrier (all of s landed;
+     * every wave is done with the other buffer), issue s + 1 into it,
+     * compute s */
+    rt_issue(st0, xb, wb, src, 0u, wave);
     for (uint32_t s = 0; s < nsteps; s += 2u) {
-        const uint32_t k2 = 2u * kRK * (s + 2u < last ? s + 2u : last);
-        const uint32_t k3 = 2u * kRK * (s + 3u < last ? s + 3u : last);
-        rt_load(a0, a1, b0, b1, xb, wb, ao, bo, k2);
-        rt_compute(acc, lds[0], a_off, b_off);
-        rt_store(lds[1], soff, p0, p1, q0, q1);
-        __syncthreads();
+        wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        if (s + 1u < nsteps) rt_issue(st1, xb, wb, src, 2u * kRK * (s + 1u), wave);
+        step(st0);
         if (s + 1u >= nsteps) break;
-        rt_load(p0, p1, q0, q1, xb, wb, ao, bo, k3);
-        rt_compute(acc, lds[1], a_off, b_off);
-        rt_store(lds[0], soff, a0, a1, b0, b1);
-        __syncthreads();
+        wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        if (s + 2u < nsteps) rt_issue(st0, xb, wb, src, 2u * kRK * (s + 2u), wave);
+        step(st1);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -736,8 +733,9 @@ __global__ __launch_bounds__(256, 2) void router_certify_wave_kernel(CertArgs A)
 }  // namespace
 
 /* K slices of the MFMA logits: enough (tile, slice) works to spread over
- * the CUs when there are few tiles (about 512 works), at most 16; the
- * approximate logits take slices x T x E floats. */
+ * the CUs when there are few tiles (about 512 works: two blocks per CU),
+ * at most kRouterMaxSlices; the approximate logits take slices x T x E
+ * floats. */
 uint32_t router_slice_cap(uint32_t T, uint32_t E) {
     const uint32_t tiles = ((T + kRT - 1u) / kRT) * ((E + kRT - 1u) / kRT);
     const uint32_t S = tiles ? 512u / tiles : 1u;
