@@ -302,11 +302,99 @@ __device__ __forceinline__ float sigmoid_slope_bound(float m) {
     return __fmul_rn(__fmul_rn(__fmul_rn(e, r), r), 1.0f + 1.0f / 1024.0f);
 }
 
-/* Scratch of one certify block (one token). */
+/* The k-th largest (with multiplicity) of the wave's keys, key[j] of lane l
+ * for expert l + 64 j; 0 when fewer than k keys are nonzero. The k-th
+ * largest lane maximum M is a lower bound (the k lanes with the largest
+ * maxima hold k keys >= M), so only the keys >= M -- a few dozen -- are
+ * ranked, one per lane from `scratch` (64 words); more than 64 of them
+ * (heavy ties) take a 32-step bitwise search over every key. */
+__device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[kTopkSlots], uint32_t k,
+                                                    uint32_t *scratch) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t lmax = 0u;
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) lmax = key[j] > lmax ? key[j] : lmax;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t t = m | (1u << b);
+        if ((uint32_t)__popcll(__ballot(lmax >= t)) >= k) m = t;
+    }
+    uint32_t mine = 0u;
+#pragma unroll
+    for (int j = 0; j < kTopkSlots; j++) mine += (m != 0u && key[j] >= m) ? 1u : 0u;
+    const uint32_t total = wave_count(mine);
+    if (m != 0u && total <= 64u) {
+        const unsigned long long below = (1ull << lane) - 1ull;
+        uint32_t pos = 0u;
+#pragma unroll
+        for (int b = 0; b < 5; b++)
+            pos += (uint32_t)__popcll(__ballot((mine >> b) & 1u) & below) << b;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++)
+            if (key[j] >= m) scratch[pos++] = key[j];
+        wave_fence();
+        const uint32_t ck = lane < total ? scratch[lane] : 0u;
+        uint32_t gt = 0u, ge = 0u;
+        for (uint32_t i = 0; i < total; i++) {
+            const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)i);
+            gt += o > ck ? 1u : 0u;
+            ge += o >= ck ? 1u : 0u;
+        }
+        wave_fence(); /* scratch is reused by the caller */
+        const unsigned long long hit = __ballot(lane < total && gt < k && k <= ge);
+        return (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)(__ffsll((long long)hit) - 1));
+    }
+    uint32_t thr = 0u;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t tt = thr | (1u << b);
+        uint32_t cnt = 0u;
+#pragma unroll
+        for (int j = 0; j < kTopkSlots; j++) cnt += key[j] >= tt ? 1u : 0u;
+        if (wave_count(cnt) >= k) thr = tt;
+    }
+    return thr;
+}
+
+/* The selection of both certification kernels, by one wave: the ncand
+ * candidates in sm.cand_id / cand_score (bias) / cand_key (exact logit
+ * bits) get their exact keys (router_sigmoid + bias) and weight scores
+ * (det_sigmoid), are compacted to keys != 0 (a NaN choice is never
+ * selected) and ranked by topk_rank_write: the exact router's top-k over
+ * keys that are 0 off the candidate list. */
+__device__ __forceinline__ void certify_select(const CertArgs &A, uint32_t t, uint32_t ncand,
+                                               TopkWaveSmem &sm) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    uint32_t nlive = 0u;
+    for (uint32_t base = 0; base < ncand; base += 64u) {
+        const uint32_t p = base + lane;
+        const bool live = p < ncand;
+        const float l = live ? __uint_as_float(sm.cand_key[p]) : 0.0f;
+        const uint32_t e = live ? sm.cand_id[p] : 0u;
+        const float b = live ? sm.cand_score[p] : 0.0f;
+        const uint32_t kk = live ? choice_key(router_sigmoid(l), b) : 0u;
+        const float sc = det_sigmoid(l);
+        const unsigned long long okm = __ballot(kk != 0u);
+        const uint32_t q = nlive + (uint32_t)__popcll(okm & below);
+        if (kk != 0u) {
+            sm.cand_key[q] = kk;
+            sm.cand_id[q] = e;
+            sm.cand_score[q] = sc;
+        }
+        nlive += (uint32_t)__popcll(okm);
+    }
+    wave_fence();
+    const uint64_t o = (uint64_t)t * A.k;
+    topk_rank_write(nlive, A.k, A.scale, A.ids + o, A.weights + o, A.ids2 ? A.ids2 + o : nullptr,
+                    A.w2 ? A.w2 + o : nullptr, sm, TopkNoHooks{});
+}
+
+/* Scratch of one certify block (one token). The candidates live in
+ * topk.cand_id (ids), cand_score (biases until the selection) and cand_key
+ * (exact logit bits until the selection), in candidate order. */
 struct CertSmem {
-    uint4 x[64 * kTopkSlots];       /* the token's row, 8-element chunks */
-    uint32_t cand[64 * kTopkSlots]; /* candidate expert ids */
-    uint32_t logit[64 * kTopkSlots]; /* exact logit bits by expert (NaN: none) */
+    uint4 x[64 * kTopkSlots]; /* the token's row, 8-element chunks */
     uint32_t ncand;
     TopkWaveSmem topk;
 };
@@ -379,14 +467,7 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
             }
         }
         /* the k-th largest approximate key */
-        uint32_t thr = 0u;
-        for (int b = 31; b >= 0; b--) {
-            const uint32_t tt = thr | (1u << b);
-            uint32_t cnt = 0u;
-#pragma unroll
-            for (int j = 0; j < kTopkSlots; j++) cnt += key[j] >= tt ? 1u : 0u;
-            if (wave_count(cnt) >= A.k) thr = tt;
-        }
+        const uint32_t thr = kth_largest_key(key, A.k, sm.topk.cand_key);
         /* E_k: the largest error bound among the experts at or above it */
         float ek = 0.0f;
 #pragma unroll
@@ -418,9 +499,11 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
         }
 #pragma unroll
         for (int j = 0; j < kTopkSlots; j++) {
-            const uint32_t e = lane + 64u * (uint32_t)j;
-            if (cand[j]) sm.cand[pos++] = e;
-            if (e < E) sm.logit[e] = kNanBits;
+            if (cand[j]) {
+                sm.topk.cand_id[pos] = lane + 64u * (uint32_t)j;
+                sm.topk.cand_score[pos] = bs[j];
+                pos++;
+            }
         }
         if (lane == 0u) sm.ncand = ncand;
     }
@@ -454,91 +537,22 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
         return wave_sum_rows<1>(s1);
     };
     uint4 wa[kTopkSlots], wb[kTopkSlots];
-    if (wave < ncand) load_row(sm.cand[wave], wa);
+    const uint32_t *cid = sm.topk.cand_id;
+    if (wave < ncand) load_row(cid[wave], wa);
     for (uint32_t p = wave; p < ncand; p += 8u) {
         /* rows p (in wa) and p + 4 (into wb, issued before p's FMAs) */
         const bool second = p + 4u < ncand;
-        if (second) load_row(sm.cand[p + 4u], wb);
+        if (second) load_row(cid[p + 4u], wb);
         const float l1 = dot_row(wa);
-        if (lane == 0u) sm.logit[sm.cand[p]] = __float_as_uint(l1);
+        if (lane == 0u) sm.topk.cand_key[p] = __float_as_uint(l1);
         if (!second) break;
-        if (p + 8u < ncand) load_row(sm.cand[p + 8u], wa);
+        if (p + 8u < ncand) load_row(cid[p + 8u], wa);
         const float l2 = dot_row(wb);
-        if (lane == 0u) sm.logit[sm.cand[p + 4u]] = __float_as_uint(l2);
+        if (lane == 0u) sm.topk.cand_key[p + 4u] = __float_as_uint(l2);
     }
     __syncthreads();
     if (wave != 0u) return;
-    /* exact keys (key 0 off the candidate list), then the exact selection */
-    uint32_t key[kTopkSlots];
-    float score[kTopkSlots];
-#pragma unroll
-    for (int j = 0; j < kTopkSlots; j++) {
-        const uint32_t e = lane + 64u * (uint32_t)j;
-        key[j] = 0u;
-        score[j] = 0.0f;
-        if (e < E) {
-            const float l = __uint_as_float(sm.logit[e]);
-            score[j] = det_sigmoid(l);
-            key[j] = choice_key(router_sigmoid(l), A.bias[e]);
-        }
-    }
-    const uint64_t o = (uint64_t)t * A.k;
-    topk_select_wave(key, score, A.k, A.scale, A.ids + o, A.weights + o,
-                     A.ids2 ? A.ids2 + o : nullptr, A.w2 ? A.w2 + o : nullptr, sm.topk);
-}
-
-/* The k-th largest (with multiplicity) of the wave's keys, key[j] of lane l
- * for expert l + 64 j; 0 when fewer than k keys are nonzero. The k-th
- * largest lane maximum M is a lower bound (the k lanes with the largest
- * maxima hold k keys >= M), so only the keys >= M -- a few dozen -- are
- * ranked, one per lane from `scratch` (64 words); more than 64 of them
- * (heavy ties) take a 32-step bitwise search over every key. */
-__device__ __forceinline__ uint32_t kth_largest_key(const uint32_t (&key)[kTopkSlots], uint32_t k,
-                                                    uint32_t *scratch) {
-    const uint32_t lane = threadIdx.x & 63u;
-    uint32_t lmax = 0u;
-#pragma unroll
-    for (int j = 0; j < kTopkSlots; j++) lmax = key[j] > lmax ? key[j] : lmax;
-    uint32_t m = 0u;
-#pragma unroll
-    for (int b = 31; b >= 0; b--) {
-        const uint32_t t = m | (1u << b);
-        if ((uint32_t)__popcll(__ballot(lmax >= t)) >= k) m = t;
-    }
-    uint32_t mine = 0u;
-#pragma unroll
-    for (int j = 0; j < kTopkSlots; j++) mine += (m != 0u && key[j] >= m) ? 1u : 0u;
-    const uint32_t total = wave_count(mine);
-    if (m != 0u && total <= 64u) {
-        const unsigned long long below = (1ull << lane) - 1ull;
-        uint32_t pos = 0u;
-#pragma unroll
-        for (int b = 0; b < 5; b++)
-            pos += (uint32_t)__popcll(__ballot((mine >> b) & 1u) & below) << b;
-#pragma unroll
-        for (int j = 0; j < kTopkSlots; j++)
-            if (key[j] >= m) scratch[pos++] = key[j];
-        wave_fence();
-        const uint32_t ck = lane < total ? scratch[lane] : 0u;
-        uint32_t gt = 0u, ge = 0u;
-        for (uint32_t i = 0; i < total; i++) {
-            const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)i);
-            gt += o > ck ? 1u : 0u;
-            ge += o >= ck ? 1u : 0u;
-        }
-        wave_fence(); /* scratch is reused by the caller */
-        const unsigned long long hit = __ballot(lane < total && gt < k && k <= ge);
-        return (uint32_t)__builtin_amdgcn_readlane((int)ck, (int)(__ffsll((long long)hit) - 1));
-    }
-    uint32_t thr = 0u;
-    for (int b = 31; b >= 0; b--) {
-        const uint32_t tt = thr | (1u << b);
-        uint32_t cnt = 0u;
-#pragma unroll
-        for (int j = 0; j < kTopkSlots; j++) cnt += key[j] >= tt ? 1u : 0u;
-        if (wave_count(cnt) >= k) thr = tt;
-    }
-    return thr;
+    certify_select(A, t, ncand, sm.topk);
 }
 
 /*
@@ -704,30 +718,7 @@ __global__ __launch_bounds__(256, 2) void router_certify_wave_kernel(CertArgs A)
         if (lane == 0u) sm.cand_key[p + 1u] = __float_as_uint(l2);
     }
     wave_fence();
-    /* exact keys and weight scores of the candidates, compacted to keys
-     * != 0 (a NaN choice is never selected) */
-    uint32_t nlive = 0u;
-    for (uint32_t base = 0; base < ncand; base += 64u) {
-        const uint32_t p = base + lane;
-        const bool live = p < ncand;
-        const float l = live ? __uint_as_float(sm.cand_key[p]) : 0.0f;
-        const uint32_t e = live ? sm.cand_id[p] : 0u;
-        const float b = live ? sm.cand_score[p] : 0.0f;
-        const uint32_t kk = live ? choice_key(router_sigmoid(l), b) : 0u;
-        const float sc = det_sigmoid(l);
-        const unsigned long long okm = __ballot(kk != 0u);
-        const uint32_t q = nlive + (uint32_t)__popcll(okm & below);
-        if (kk != 0u) {
-            sm.cand_key[q] = kk;
-            sm.cand_id[q] = e;
-            sm.cand_score[q] = sc;
-        }
-        nlive += (uint32_t)__popcll(okm);
-    }
-    wave_fence();
-    const uint64_t o = (uint64_t)t * A.k;
-    topk_rank_write(nlive, A.k, A.scale, A.ids + o, A.weights + o, A.ids2 ? A.ids2 + o : nullptr,
-                    A.w2 ? A.w2 + o : nullptr, sm, TopkNoHooks{});
+    certify_select(A, t, ncand, sm);
 }
 
 }  // namespace
