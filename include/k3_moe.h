@@ -32,9 +32,10 @@ extern "C" {
  * [rows, columns / 32]. Fields follow the six-tensor span order of
  * k3_prefill.c:71-75 (w1 = gate, w2 = down, w3 = up). Tensors must start
  * 8-byte aligned; the 8-mod-16 starts of real checkpoint spans
- * (k3_rocm_ops.cu:207-223) are read as 8-byte pairs, and under the MXFP8
- * precisions an expert with any tensor that is not 16-byte aligned runs on
- * the exact kernels (the MFMA kernels stage 16-byte pieces).
+ * (k3_rocm_ops.cu:207-223) are read as 8-byte pairs by the exact kernels
+ * and as 16-byte direct-to-LDS pieces (which take 8-byte aligned sources
+ * on gfx950) by the MFMA kernels, with the same results as aligned
+ * tensors.
  */
 typedef struct {
     const void *gate_packed;  /* w1.weight_packed [ffn, hidden / 2]  */

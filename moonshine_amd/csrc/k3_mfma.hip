@@ -239,10 +239,13 @@ void launch_split_rows(const MfmaBuffers &B, const uint16_t *x, uint32_t rows, u
 /* One block of 1024 threads (thread e = expert e). Class 0: experts with
  * <= 16 rows (one 16-row tile), class 1: <= 64 rows (one 64-row tile),
  * class 2: <= 96 rows (one 96-row tile), class 3: 128-row tiles (the last
- * one partial). Tiles are listed in expert order. For the MFMA kernels
- * (all == 0) an expert with a tensor that is not 16-byte aligned (the
- * 8-mod-16 starts of real checkpoint spans) gets no tiles: direct-to-LDS
- * loads move 16-byte pieces, so B.unaligned hands it to the exact grouped
+ * one partial). Tiles are listed in expert order. The 8-mod-16 tensor
+ * starts of real checkpoint spans (about a quarter of the shipped tensors,
+ * k3_rocm_ops.cu:207-223) take the MFMA kernels like aligned ones: the
+ * 16-byte direct-to-LDS loads return the right bytes from 8-byte aligned
+ * sources on gfx950 (measured, register and LDS forms). For the MFMA
+ * kernels (all == 0) an expert with a tensor that is not even 8-byte
+ * aligned gets no tiles, and B.unaligned hands it to the exact grouped
  * kernels. With all != 0 (the exact kernels' own tile list) every selected
  * expert gets tiles. */
 __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(1024) void tile_build_kernel(MfmaBuffers B,
         const k3_moe_expert ex = experts[e];
         odd = (((uintptr_t)ex.gate_packed | (uintptr_t)ex.gate_scales | (uintptr_t)ex.down_packed |
                 (uintptr_t)ex.down_scales | (uintptr_t)ex.up_packed | (uintptr_t)ex.up_scales) %
-               16u) != 0u;
+               8u) != 0u;
     }
     if (odd) B.unaligned[1u + atomicAdd(&odd_count, 1u)] = e;
     constexpr int kLast = kTileClasses - 1; /* the multi-tile class */

@@ -623,7 +623,7 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
                                  ws.token_index, ws.route_index, experts, s, T,
                                  precision == K3_MOE_MFMA ? 2u : 1u, st, mark))
             return false;
-        /* experts with a tensor that is not 16-byte aligned (no MFMA tiles):
+        /* experts with a tensor that is not 8-byte aligned (no MFMA tiles):
          * the exact kernels, after the MFMA down kernel has consumed the
          * activation codes that share `act` */
         const uint32_t walk = upper < kFallbackExperts ? upper : kFallbackExperts;

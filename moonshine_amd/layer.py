@@ -38,9 +38,10 @@ class ExpertStore:
     """
 
     def __init__(self, experts, hidden, ffn, seed, device="cuda", misalign=0, misalign_odd=False):
-        """misalign (0 or 8): start every tensor 8 bytes past a 16-byte
-        boundary, as real checkpoint spans do (k3_rocm_ops.cu:207-223);
-        misalign_odd: only the tensors of odd experts."""
+        """misalign (0, 4 or 8): start every tensor that many bytes past a
+        16-byte boundary (8: as real checkpoint spans do,
+        k3_rocm_ops.cu:207-223); misalign_odd: only the tensors of odd
+        experts."""
         self.experts, self.hidden, self.ffn, self.seed = experts, hidden, ffn, seed
         self.sizes = expert_tensor_sizes(hidden, ffn)
         self.offsets = []
@@ -59,11 +60,18 @@ class ExpertStore:
             shift = misalign if (not misalign_odd or e % 2 == 1) else 0
             self.shifts.append(shift)
             for j, (o, s) in enumerate(zip(self.offsets, self.sizes)):
-                ptr = base + e * self.span + o + shift
+                start = e * self.span + o + shift
+                ptr = base + start
                 table[e, j] = ptr
-                if not lib().k3_moe_synth_fill(ctypes.c_void_p(ptr), s, seed, e * 8 + j, j & 1,
+                # the generator writes from 8-byte aligned starts: other
+                # shifts are filled aligned and copied into place
+                tmp = None if shift % 8 == 0 else torch.empty(s, dtype=torch.uint8, device=device)
+                dst = ptr if tmp is None else tmp.data_ptr()
+                if not lib().k3_moe_synth_fill(ctypes.c_void_p(dst), s, seed, e * 8 + j, j & 1,
                                                stream):
                     raise RuntimeError("k3_moe_synth_fill failed")
+                if tmp is not None:
+                    self.buffer[start:start + s].copy_(tmp)
         self.table = torch.from_numpy(table.view(np.int64)).to(device)
 
     def host_expert(self, e):
