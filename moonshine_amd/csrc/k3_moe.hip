@@ -369,25 +369,31 @@ __device__ __forceinline__ void gateup_rows(uint16_t *__restrict__ act,
     }
 }
 
-/* grid (F / (4 * RW), walk), block 256 (ExactWork). */
+/* grid (up to F / (4 * RW), walk), block 256 (ExactWork); column blocks
+ * past the grid's x extent are walked (the hand-off list, usually empty,
+ * runs on a small grid). */
 template <int RW, int TT>
 __global__ __launch_bounds__(256, 2) void grouped_gateup_kernel(
         uint16_t *__restrict__ act, const uint16_t *__restrict__ x, ExactWork W,
         const uint32_t *__restrict__ token_index, const k3_moe_expert *__restrict__ experts,
         uint32_t H, uint32_t F, uint32_t kind, float beta, float lb) {
-    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RW;
-    if (row0 >= F) return;
-    if (!W.list) {
-        uint32_t e, base, n;
-        for (uint32_t q = blockIdx.y; exact_tile(W, q, e, base, n); q += gridDim.y)
-            gateup_rows<RW, TT>(act, x, token_index, experts[e], base, n, row0, H, F, kind, beta,
-                                lb);
-        return;
-    }
-    for (uint32_t q = blockIdx.y; q < *W.list_count; q += gridDim.y) {
-        const uint32_t e = W.list[q];
-        gateup_rows<RW, TT>(act, x, token_index, experts[e], W.offsets[e], W.counts[e], row0, H,
-                            F, kind, beta, lb);
+    const uint32_t nbx = F / (4u * RW);
+    const uint32_t listed = W.list ? *W.list_count : 0u;
+    if (W.list && blockIdx.y >= listed) return;
+    for (uint32_t bx = blockIdx.x; bx < nbx; bx += gridDim.x) {
+        const uint32_t row0 = (bx * 4u + (threadIdx.x >> 6)) * RW;
+        if (!W.list) {
+            uint32_t e, base, n;
+            for (uint32_t q = blockIdx.y; exact_tile(W, q, e, base, n); q += gridDim.y)
+                gateup_rows<RW, TT>(act, x, token_index, experts[e], base, n, row0, H, F, kind,
+                                    beta, lb);
+            continue;
+        }
+        for (uint32_t q = blockIdx.y; q < listed; q += gridDim.y) {
+            const uint32_t e = W.list[q];
+            gateup_rows<RW, TT>(act, x, token_index, experts[e], W.offsets[e], W.counts[e], row0,
+                                H, F, kind, beta, lb);
+        }
     }
 }
 
@@ -440,7 +446,8 @@ __device__ __forceinline__ void down_rows(uint16_t *__restrict__ y,
     }
 }
 
-/* grid (H / (4 * RB), walk), block 256: y[route] = down_e . act[row]. Two
+/* grid (up to H / (4 * RB), walk), block 256: y[route] = down_e . act[row]
+ * (column blocks walked as in grouped_gateup_kernel). Two
  * waves per SIMD (at most 256 VGPRs): at one wave per SIMD (269 VGPRs) the
  * kernel took 15.0 against 8.7 ms at cfg3. */
 template <int RB, int TT>
@@ -448,17 +455,22 @@ __global__ __launch_bounds__(256, 2) void grouped_down_kernel(
         uint16_t *__restrict__ y, const uint16_t *__restrict__ act, ExactWork W,
         const uint32_t *__restrict__ route_index, const k3_moe_expert *__restrict__ experts,
         uint32_t H, uint32_t F) {
-    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * RB;
-    if (row0 >= H) return;
-    if (!W.list) {
-        uint32_t e, base, n;
-        for (uint32_t q = blockIdx.y; exact_tile(W, q, e, base, n); q += gridDim.y)
-            down_rows<RB, TT>(y, act, route_index, experts[e], base, n, row0, H, F);
-        return;
-    }
-    for (uint32_t q = blockIdx.y; q < *W.list_count; q += gridDim.y) {
-        const uint32_t e = W.list[q];
-        down_rows<RB, TT>(y, act, route_index, experts[e], W.offsets[e], W.counts[e], row0, H, F);
+    const uint32_t nbx = H / (4u * RB);
+    const uint32_t listed = W.list ? *W.list_count : 0u;
+    if (W.list && blockIdx.y >= listed) return;
+    for (uint32_t bx = blockIdx.x; bx < nbx; bx += gridDim.x) {
+        const uint32_t row0 = (bx * 4u + (threadIdx.x >> 6)) * RB;
+        if (!W.list) {
+            uint32_t e, base, n;
+            for (uint32_t q = blockIdx.y; exact_tile(W, q, e, base, n); q += gridDim.y)
+                down_rows<RB, TT>(y, act, route_index, experts[e], base, n, row0, H, F);
+            continue;
+        }
+        for (uint32_t q = blockIdx.y; q < listed; q += gridDim.y) {
+            const uint32_t e = W.list[q];
+            down_rows<RB, TT>(y, act, route_index, experts[e], W.offsets[e], W.counts[e], row0,
+                              H, F);
+        }
     }
 }
 
@@ -591,10 +603,13 @@ DecodeParams decode_params(const Workspace &ws, void *output, const void *hidden
     return P;
 }
 
-/* Experts the MFMA path hands to the exact kernels (tensors not 16-byte
+/* Experts the MFMA path hands to the exact kernels (tensors not 8-byte
  * aligned) are walked by a grid of this many expert rows: with none, the
  * blocks exit at once. */
 constexpr uint32_t kFallbackExperts = 8;
+/* column blocks of the hand-off grid (each walks the rest): an empty list
+ * then costs a launch of 8 x 32 blocks, not thousands */
+constexpr uint32_t kFallbackCols = 32;
 
 /* Expert stage on routes already in ws.ids / ws.weights. */
 bool run_experts(const Workspace &ws, void *output, const void *hidden, const void *residual,
@@ -627,16 +642,18 @@ bool run_experts(const Workspace &ws, void *output, const void *hidden, const vo
          * the exact kernels, after the MFMA down kernel has consumed the
          * activation codes that share `act` */
         const uint32_t walk = upper < kFallbackExperts ? upper : kFallbackExperts;
+        const uint32_t gx = F / (4u * RW) < kFallbackCols ? F / (4u * RW) : kFallbackCols;
+        const uint32_t dx = H / (4u * RB) < kFallbackCols ? H / (4u * RB) : kFallbackCols;
         ExactWork W{};
         W.list_count = ws.mfma.unaligned;
         W.list = ws.mfma.unaligned + 1;
         W.counts = ws.counts;
         W.offsets = ws.offsets;
         hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_gateup_kernel<RW, TT>),
-                           dim3(F / (4u * RW), walk), dim3(256), 0, st, ws.act,
+                           dim3(gx, walk), dim3(256), 0, st, ws.act,
                            (const uint16_t *)hidden, W, ws.token_index, experts, H, F,
                            s.activation, beta, lb);
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TD>), dim3(H / (4u * RB), walk),
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(grouped_down_kernel<RB, TD>), dim3(dx, walk),
                            dim3(256), 0, st, ws.y, ws.act, W, ws.route_index, experts, H, F);
         mark(K3_MOE_STAGE_COMBINE);
         hipLaunchKernelGGL(combine_kernel, dim3((H / 8u + kCombineThreads - 1u) / kCombineThreads, T),
