@@ -406,7 +406,8 @@ struct CertSmem {
  * 64, ... -- the chunks it owns in that order -- from the block's copy of
  * the row in LDS, and the next candidate row's loads are issued before the
  * current row's FMAs, so two rows are in flight); wave 0 turns them into
- * keys (key 0 off the list) and runs the exact selection.
+ * keys and ranks them (certify_select; every other expert has key 0).
+ * Used for batches below kCertWaveMinTokens.
  */
 __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
     __shared__ CertSmem sm;
