@@ -277,7 +277,7 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to
  * workgroups and no workgroup is launched past the tile count. List mode:
  * list = (count, expert ids), walked the same way, each expert's rows
  * whole (the MFMA path's fallback for experts whose tensors are not
- * 16-byte aligned).
+ * 8-byte aligned).
  */
 struct ExactWork {
     const uint32_t *tiles, *tile_count;
