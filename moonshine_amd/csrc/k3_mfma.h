@@ -34,7 +34,7 @@ struct MfmaBuffers {
     uint32_t *tiles;            /* kTileClasses x tile_cap x {expert, row0, rows} */
     uint32_t *tile_count;       /* [kTileClasses] */
     uint32_t *unaligned;        /* [E + 1]: count, then the selected experts with a
-                                   tensor that is not 16-byte aligned (any order) */
+                                   tensor that is not 8-byte aligned (any order) */
     uint32_t tile_cap[kTileClasses];
 };
 
