@@ -280,6 +280,9 @@ def main():
     ap.add_argument("--streams", type=int, default=1, choices=(1, 2),
                     help="--native: 2 runs the latent projection and the shared expert's gate/up "
                          "on a second stream (host-bound when not in a graph)")
+    ap.add_argument("--misalign", action="store_true",
+                    help="start the odd experts' tensors 8 bytes past a 16-byte boundary, as "
+                         "about a quarter of a real checkpoint's tensors do")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the extra HIP-graph replay figure (`graph` in the JSON line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -343,7 +346,11 @@ def run_layer(args, cfg, T, precision, steps, warmup, R, with_cpu, cpu_budget=No
     log(f"bench: {cfg.name} T={T} building resident expert store ...")
     torch.cuda.empty_cache()
     inputs = make_inputs(cfg, tokens=T * R)
-    moe = L.build_layer(cfg, inputs, device="cuda")
+    store = None
+    if getattr(args, "misalign", False):  # odd experts' tensors at 8 mod 16
+        store = L.ExpertStore(cfg.experts, cfg.hidden, cfg.ffn, seed=cfg.seed, device="cuda",
+                              misalign=8, misalign_odd=True)
+    moe = L.build_layer(cfg, inputs, device="cuda", store=store)
     xs = L.bf16_tensor(inputs.hidden).view(R, T, cfg.hidden)
     rs = L.bf16_tensor(inputs.residual).view(R, T, cfg.hidden)
     out = torch.empty((T, cfg.hidden), dtype=xs.dtype, device=xs.device)
