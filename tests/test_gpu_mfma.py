@@ -295,3 +295,24 @@ def test_shapes_vs_exact(cuda, T, H, F, E, k):
     np.testing.assert_array_equal(ids, ids_e)
     np.testing.assert_array_equal(w, w_e)
     assert_close(out, exact, f"{cfg.name} mfma vs exact")
+
+
+def test_k3_shape_mixed_alignment_bitexact(cuda):
+    """The K3 shape (hidden 7168, ffn 2048, 896 experts, top-16) at 300
+    tokens, every tile class populated, with the odd experts' tensors at 8
+    mod 16 (real checkpoint spans): the MFMA path stages them by the same
+    16-byte direct-to-LDS loads and gives the bits of the aligned store."""
+    cfg = dataclasses.replace(CONFIGS[1], name="k3-300-mixed", tokens=300)
+    inputs = make_inputs(cfg, tokens=300)
+    ref, ids_a, w_a = forward(get_layer(cfg, inputs, cuda), inputs, cuda, MFMA)
+    mixed = L.ExpertStore(cfg.experts, cfg.hidden, cfg.ffn, seed=cfg.seed, device=cuda,
+                          misalign=8, misalign_odd=True)
+    try:
+        got, ids_m, w_m = forward(L.build_layer(cfg, inputs, device=cuda, store=mixed), inputs,
+                                  cuda, MFMA)
+    finally:
+        del mixed
+        torch.cuda.empty_cache()
+    np.testing.assert_array_equal(ids_m, ids_a)
+    np.testing.assert_array_equal(w_m, w_a)
+    np.testing.assert_array_equal(got, ref)
