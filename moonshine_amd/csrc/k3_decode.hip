@@ -2,8 +2,8 @@
  * Single-token decode of the routed-MoE layer on gfx950: five kernels.
  *
  *   router_kernel   2 expert rows per one-wave block (the hidden state is
- *                   read once for both): logit, sigmoid score and order
- *                   key per expert.
+ *                   read once for both): logit in the reference's order,
+ *                   sigmoid score and order key per expert.
  *   topk_kernel     one wave selects the routes (k3_topk.h) and resolves
  *                   the k selected expert descriptors once (their loads
  *                   start before ranking), so the expert kernels reach
@@ -55,12 +55,13 @@ constexpr int kDownRows = 8;
 /* router                                                                  */
 /* ---------------------------------------------------------------------- */
 
-/* One wave per block computes rows 2b and 2b+1 in the w64 order (elements
- * in chunks of 8; lane l owns chunks l, l+64, ...; fmaf in column order;
- * wave64 butterfly). Both weight rows and the hidden state are loaded in
- * one batch (one memory round trip), and the hidden state is read once
- * for the two rows: a CU's L2 read bandwidth, not HBM, bounds this kernel,
- * so rereading x per row would cost as much as a third of the weights. */
+/* One wave per block computes rows 2b and 2b+1 in the reference's order
+ * (ref_chunk: 16-byte chunks l, l+64, ... per lane, the reference's 256
+ * partials four per lane, then its tree). Both weight rows and the hidden
+ * state are loaded in one batch (one memory round trip), and the hidden
+ * state is read once for the two rows: a CU's L2 read bandwidth, not HBM,
+ * bounds this kernel, so rereading x per row would cost as much as a third
+ * of the weights. */
 __global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
     const uint32_t lane = threadIdx.x;
     const uint32_t chunks = P.router_cols / 8u;
@@ -78,25 +79,15 @@ __global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
         wb[j] = gload_nt(w1 + c);
         xv[j] = x4[c];
     }
-    float a = 0.0f, b = 0.0f;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < kRouterMaxChunks; j++) {
         if (lane + 64u * j < chunks) {
-            const float x8[8] = {bf16_lo(xv[j].x), bf16_hi(xv[j].x), bf16_lo(xv[j].y),
-                                 bf16_hi(xv[j].y), bf16_lo(xv[j].z), bf16_hi(xv[j].z),
-                                 bf16_lo(xv[j].w), bf16_hi(xv[j].w)};
-            const uint32_t pa[4] = {wa[j].x, wa[j].y, wa[j].z, wa[j].w};
-            const uint32_t pb[4] = {wb[j].x, wb[j].y, wb[j].z, wb[j].w};
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                a = fmaf(bf16_lo(pa[q]), x8[2 * q], a);
-                a = fmaf(bf16_hi(pa[q]), x8[2 * q + 1], a);
-                b = fmaf(bf16_lo(pb[q]), x8[2 * q], b);
-                b = fmaf(bf16_hi(pb[q]), x8[2 * q + 1], b);
-            }
+            ref_chunk(a, j, wa[j], xv[j]);
+            ref_chunk(b, j, wb[j], xv[j]);
         }
     }
-    const float va = wave_sum(a), vb = wave_sum(b);
+    const float va = ref_logit_finish(a), vb = ref_logit_finish(b);
     if (lane < (two ? 2u : 1u)) {
         const uint32_t row = row0 + lane;
         const float v = lane ? vb : va;

@@ -266,6 +266,48 @@ __device__ __forceinline__ int wave_rows_owner() {
     return row;
 }
 
+/* ---- router logits in the reference's order ------------------------------ */
+
+/*
+ * k3_bf16_gemv_kernel<float> and the tiled GEMM's quad path
+ * (k3_rocm_ops.cu:359-425, 512-661): 256 threads, thread t sums the 4-element
+ * quads t, t + 256, ... into its partial, then an LDS tree 128 -> 1. The
+ * reference is built with -ffast-math; hipcc (ROCm 7.2, gfx950) turns the
+ * quad expression into v_pk_mul_f32 (w2 x2, w3 x3), v_pk_fma_f32 (w1 x1 +
+ * w2 x2, w0 x0 + w3 x3) and two adds, so a quad adds (p1 + p2) + (p0 + p3)
+ * to the partial, every step rounded to fp32. The products are exact (bf16
+ * x bf16), so each multiply here rounds nothing it does not round there.
+ */
+__device__ __forceinline__ float ref_quad(uint32_t wlo, uint32_t whi, uint32_t xlo,
+                                          uint32_t xhi) {
+    const float p2 = __fmul_rn(bf16_lo(whi), bf16_lo(xhi));
+    const float p3 = __fmul_rn(bf16_hi(whi), bf16_hi(xhi));
+    const float a = fmaf(bf16_hi(wlo), bf16_hi(xlo), p2);
+    const float b = fmaf(bf16_lo(wlo), bf16_lo(xlo), p3);
+    return __fadd_rn(a, b);
+}
+
+/* 16-byte chunk c = lane + 64 j of a row: its quads 2c and 2c + 1 belong to
+ * the reference's partials 2 lane + 128 (j & 1) and that + 1 (the quads of
+ * a partial arrive in j order, as its thread adds them), kept in
+ * acc[2 (j & 1)] and acc[2 (j & 1) + 1]. */
+__device__ __forceinline__ void ref_chunk(float (&acc)[4], int j, uint4 w, uint4 x) {
+    const int s = 2 * (j & 1);
+    acc[s] = __fadd_rn(acc[s], ref_quad(w.x, w.y, x.x, x.y));
+    acc[s + 1] = __fadd_rn(acc[s + 1], ref_quad(w.z, w.w, x.z, x.w));
+}
+
+/* The reference's tree over the four partials of every lane (ref_chunk):
+ * level 128 adds acc[0] + acc[2] and acc[1] + acc[3] (partials t and t +
+ * 128) in the lane; levels 64 .. 2 pair partials 2 lane and 2 lane + 2^k,
+ * i.e. lanes lane ^ 32 .. lane ^ 1 (a wave64 butterfly of each); level 1
+ * adds the lane's two results. Every lane returns the logit. */
+__device__ __forceinline__ float ref_logit_finish(const float (&acc)[4]) {
+    const float r0 = wave_sum(__fadd_rn(acc[0], acc[2]));
+    const float r1 = wave_sum(__fadd_rn(acc[1], acc[3]));
+    return __fadd_rn(r0, r1);
+}
+
 /* ---- MXFP8 (E4M3 codes + E8M0 block scales) ------------------------------ */
 
 /* floor(log2(a)) of a finite a > 0 (normal or subnormal). */

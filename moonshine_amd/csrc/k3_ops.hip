@@ -109,6 +109,115 @@ bool launch_bf16_rows_f32(void *out, const void *w, const void *x, uint32_t toke
 }
 
 /*
+ * Router logits (f32 output) in the reference's order, k3_rocm_ops.cu:359-425
+ * and 512-661: thread t of 256 sums the quads t, t + 256, ...; the quad's
+ * arithmetic is ref_quad; the LDS tree 128 -> 1 finishes. One wave per
+ * weight row and TT tokens per wave (the token tile changes no bit).
+ *   vec (16-byte rows): chunk c = lane + 64 j holds quads 2c and 2c + 1
+ *     (ref_chunk); the four partials of each token meet in
+ *     wave_sum_rows<2 TT> (rows 2t, 2t + 1 = levels 128 .. 2 of token t) and
+ *     the last level adds rows 2t and 2t + 1, which sit 32 / TT lanes apart.
+ *   otherwise: lane l owns partials l, l + 64, l + 128, l + 192, each summed
+ *     as the reference's quad (cols % 4 == 0), pair (cols % 2 == 0: p1 then
+ *     p0, :395-405) or element (fmaf, :407-411) path, from scalar loads;
+ *     levels 128 and 64 in the lane, then wave_sum_rows<TT>.
+ */
+template <int TT>
+__global__ __launch_bounds__(256) void bf16_rows_ref_kernel(
+        float *__restrict__ out, const uint16_t *__restrict__ weights,
+        const uint16_t *__restrict__ input, uint32_t tokens, uint32_t rows, uint32_t cols,
+        uint32_t vec_ok) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const uint32_t t0 = blockIdx.y * TT;
+    if (row >= rows) return;
+    const uint32_t active = tokens - t0 < (uint32_t)TT ? tokens - t0 : (uint32_t)TT;
+    const uint16_t *w = weights + (uint64_t)row * cols;
+    float v;
+    int owner;
+    if (vec_ok) {
+        float acc[TT][4];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
+        const uint4 *w4 = (const uint4 *)w;
+        const uint32_t chunks = cols / 8u;
+        for (uint32_t c = lane, j = 0; c < chunks; c += 64u, j++) {
+            const uint4 wv = w4[c];
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+                if ((uint32_t)t < active)
+                    ref_chunk(acc[t], (int)(j & 1u),  wv,
+                              ((const uint4 *)(input + (uint64_t)(t0 + t) * cols))[c]);
+        }
+        float p[2 * TT];
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            p[2 * t] = __fadd_rn(acc[t][0], acc[t][2]);
+            p[2 * t + 1] = __fadd_rn(acc[t][1], acc[t][3]);
+        }
+        v = wave_sum_rows<2 * TT>(p);
+        v = __fadd_rn(v, __shfl_xor(v, 32 / TT, 64));
+        owner = wave_rows_owner<2 * TT>() / 2;
+    } else {
+        const uint32_t mode = cols % 4u == 0u ? 0u : cols % 2u == 0u ? 1u : 2u;
+        const uint32_t step = mode == 0u ? 4u : mode == 1u ? 2u : 1u;
+        const uint32_t units = cols / step;
+        float part[TT][4];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int m = 0; m < 4; m++) part[t][m] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            for (uint32_t u = lane + 64u * (uint32_t)m; u < units; u += 256u) {
+                const uint16_t *wu = w + (uint64_t)u * step;
+                float wf[4];
+                for (uint32_t i = 0; i < step; i++) wf[i] = bf16_to_f32(wu[i]);
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    if ((uint32_t)t >= active) continue;
+                    const uint16_t *xu = input + (uint64_t)(t0 + t) * cols + (uint64_t)u * step;
+                    float s = part[t][m];
+                    if (mode == 0u) {
+                        const float p2 = __fmul_rn(wf[2], bf16_to_f32(xu[2]));
+                        const float p3 = __fmul_rn(wf[3], bf16_to_f32(xu[3]));
+                        s = __fadd_rn(s, __fadd_rn(fmaf(wf[1], bf16_to_f32(xu[1]), p2),
+                                                   fmaf(wf[0], bf16_to_f32(xu[0]), p3)));
+                    } else if (mode == 1u) {
+                        s = __fadd_rn(s, __fmul_rn(wf[1], bf16_to_f32(xu[1])));
+                        s = __fadd_rn(s, __fmul_rn(wf[0], bf16_to_f32(xu[0])));
+                    } else {
+                        s = fmaf(wf[0], bf16_to_f32(xu[0]), s);
+                    }
+                    part[t][m] = s;
+                }
+            }
+        }
+        float p[TT];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+            p[t] = __fadd_rn(__fadd_rn(part[t][0], part[t][2]), __fadd_rn(part[t][1], part[t][3]));
+        v = wave_sum_rows<TT>(p);
+        owner = wave_rows_owner<TT>();
+    }
+    const uint32_t lanes_per = 64u / TT;
+    if ((lane & (lanes_per - 1u)) == 0u && (uint32_t)owner < active)
+        out[(uint64_t)(t0 + owner) * rows + row] = v;
+}
+
+template <int TT>
+bool launch_bf16_rows_ref(float *out, const void *w, const void *x, uint32_t tokens,
+                          uint32_t rows, uint32_t cols, hipStream_t s) {
+    const uint32_t vec_ok = (cols % 8u == 0u) && (((uintptr_t)w | (uintptr_t)x) % 16u == 0u);
+    dim3 grid((rows + kWavesPerBlock - 1u) / kWavesPerBlock, (tokens + TT - 1u) / TT);
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(bf16_rows_ref_kernel<TT>), grid, dim3(kThreads), 0, s, out,
+                       (const uint16_t *)w, (const uint16_t *)x, tokens, rows, cols, vec_ok);
+    return hipGetLastError() == hipSuccess;
+}
+
+/*
  * The same w64 order for many tokens at once (router logits of a prefill
  * batch), as a register-blocked GEMM: a block computes 32 tokens x 16 rows.
  * Wave w (of 8) owns tokens 8 (w / 2) .. +8 and rows 8 (w % 2) .. +8; lane l
@@ -248,6 +357,147 @@ bool launch_bf16_gemm_w64(void *out, const void *w, const void *x, uint32_t toke
                                 : (uint64_t)token_tiles * row_tiles;
     if (blocks > 0x7fffffffull) return false;
     hipLaunchKernelGGL(HIP_KERNEL_NAME(bf16_gemm_w64_kernel<B16>), dim3((uint32_t)blocks), dim3(kGThreads), 0, s, out,
+                       (const uint16_t *)w, (const uint16_t *)x, tokens, rows, cols, row_tiles,
+                       xcd);
+    return hipGetLastError() == hipSuccess;
+}
+
+/*
+ * Router logits of many tokens (f32, T >= 128) in the reference's order as
+ * a blocked GEMM: a block computes 16 tokens x 8 weight rows; a K step is
+ * 1024 columns (256 quads), so each of the reference's 256 partials of an
+ * output gets exactly one quad per step. Wave w takes partials 64 (w % 4) +
+ * lane (its K quarter) of tokens 8 (w / 4) .. + 8 and all 8 rows: one
+ * accumulator per output, the quad summed by ref_quad, the quads of a
+ * partial in K order as the reference's thread adds them. At the end the
+ * K quarters meet in LDS as the reference's tree levels 128 (quarters q
+ * and q + 2) and 64 (quarters 0 and 1), and wave_sum_rows<64> does levels
+ * 32 .. 1. Out-of-range tokens/rows/columns stage zeros: a zero quad adds
+ * +0, which changes no partial (a partial is never -0). The step's bf16
+ * tiles are loaded into registers one step ahead and staged in LDS as fp32
+ * quads, so each fragment read is one lane-contiguous ds_read_b128. Block
+ * order is XCD-aware as in bf16_gemm_w64_kernel.
+ */
+constexpr int kQT = 16, kQE = 8, kQThreads = 512;
+
+__device__ __forceinline__ float ref_quad_f4(const float4 &w, const float4 &x) {
+    const float p2 = __fmul_rn(w.z, x.z), p3 = __fmul_rn(w.w, x.w);
+    return __fadd_rn(fmaf(w.y, x.y, p2), fmaf(w.x, x.x, p3));
+}
+
+__global__ __launch_bounds__(512) void bf16_gemm_ref_kernel(
+        float *__restrict__ out, const uint16_t *__restrict__ weights,
+        const uint16_t *__restrict__ input, uint32_t tokens, uint32_t rows, uint32_t cols,
+        uint32_t row_tiles, uint32_t xcd_groups) {
+    __shared__ float4 xs[kQT][256];
+    __shared__ float4 wsm[kQE][256];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    uint32_t tt, et;
+    {
+        const uint32_t L = blockIdx.x;
+        if (xcd_groups) {
+            const uint32_t x = L & 7u, j = L >> 3;
+            const uint32_t base = row_tiles >> 3, rem = row_tiles & 7u;
+            const uint32_t cnt = base + (x < rem ? 1u : 0u);
+            const uint32_t start = x * base + (x < rem ? x : rem);
+            const uint32_t token_tiles = (tokens + kQT - 1u) / kQT;
+            if (cnt == 0u || j >= token_tiles * cnt) return;
+            tt = j / cnt;
+            et = start + j % cnt;
+        } else {
+            tt = L / row_tiles;
+            et = L % row_tiles;
+        }
+    }
+    const uint32_t t0 = tt * kQT, e0 = et * kQE;
+    const uint32_t chunks = cols / 8u, nsteps = (chunks + 127u) / 128u;
+    const uint4 *x4 = (const uint4 *)input, *w4 = (const uint4 *)weights;
+    /* staging items: 16 token rows then 8 weight rows, 128 chunks each */
+    constexpr int kItems = (kQT + kQE) * 128 / kQThreads;
+    uint4 reg[kItems];
+    auto load_step = [&](uint32_t s) {
+#pragma unroll
+        for (int q = 0; q < kItems; q++) {
+            const uint32_t it = tid + (uint32_t)q * kQThreads;
+            const uint32_t r = it >> 7, c = 128u * s + (it & 127u);
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (r < (uint32_t)kQT) {
+                if (t0 + r < tokens && c < chunks) v = x4[(uint64_t)(t0 + r) * chunks + c];
+            } else if (e0 + r - kQT < rows && c < chunks) {
+                v = w4[(uint64_t)(e0 + r - kQT) * chunks + c];
+            }
+            reg[q] = v;
+        }
+    };
+    const uint32_t kq = wave & 3u, tg = wave >> 2, qi = 64u * kq + lane;
+    float acc[64];
+#pragma unroll
+    for (int i = 0; i < 64; i++) acc[i] = 0.0f;
+    load_step(0u);
+    for (uint32_t s = 0; s < nsteps; s++) {
+        __syncthreads(); /* the previous step's reads are done */
+#pragma unroll
+        for (int q = 0; q < kItems; q++) {
+            const uint32_t it = tid + (uint32_t)q * kQThreads;
+            const uint4 v = reg[q];
+            const float4 a = make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+            const float4 b = make_float4(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w));
+            const uint32_t r = it >> 7, c = it & 127u;
+            float4 *dst = r < (uint32_t)kQT ? &xs[r][2u * c] : &wsm[r - kQT][2u * c];
+            dst[0] = a;
+            dst[1] = b;
+        }
+        __syncthreads();
+        if (s + 1u < nsteps) load_step(s + 1u);
+        float4 wv[kQE];
+#pragma unroll
+        for (int e = 0; e < kQE; e++) wv[e] = wsm[e][qi];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 xv = xs[8u * tg + t][qi];
+#pragma unroll
+            for (int e = 0; e < kQE; e++)
+                acc[8 * t + e] = __fadd_rn(acc[8 * t + e], ref_quad_f4(wv[e], xv));
+        }
+    }
+    /* tree levels 128 and 64 across the K quarters, through LDS */
+    float *red = (float *)&xs[0][0]; /* [2 token groups][2][64 outputs][64 lanes] */
+    __syncthreads();
+    if (kq >= 2u) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) red[((tg * 2u + kq - 2u) * 64u + i) * 64u + lane] = acc[i];
+    }
+    __syncthreads();
+    if (kq < 2u) {
+#pragma unroll
+        for (int i = 0; i < 64; i++)
+            acc[i] = __fadd_rn(acc[i], red[((tg * 2u + kq) * 64u + i) * 64u + lane]);
+    }
+    __syncthreads();
+    if (kq == 1u) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) red[(tg * 64u + i) * 64u + lane] = acc[i];
+    }
+    __syncthreads();
+    if (kq != 0u) return;
+#pragma unroll
+    for (int i = 0; i < 64; i++) acc[i] = __fadd_rn(acc[i], red[(tg * 64u + i) * 64u + lane]);
+    const float v = wave_sum_rows<64>(acc);
+    const int owner = wave_rows_owner<64>();
+    const uint32_t t = t0 + 8u * tg + (uint32_t)(owner >> 3);
+    const uint32_t e = e0 + (uint32_t)(owner & 7);
+    if (t < tokens && e < rows) out[(uint64_t)t * rows + e] = v;
+}
+
+bool launch_bf16_gemm_ref(float *out, const void *w, const void *x, uint32_t tokens,
+                          uint32_t rows, uint32_t cols, hipStream_t s) {
+    const uint32_t token_tiles = (tokens + kQT - 1u) / kQT;
+    const uint32_t row_tiles = (rows + kQE - 1u) / kQE;
+    const uint32_t xcd = row_tiles >= 8u ? 1u : 0u;
+    const uint64_t blocks = xcd ? 8ull * token_tiles * ((row_tiles + 7u) / 8u)
+                                : (uint64_t)token_tiles * row_tiles;
+    if (blocks > 0x7fffffffull) return false;
+    hipLaunchKernelGGL(bf16_gemm_ref_kernel, dim3((uint32_t)blocks), dim3(kQThreads), 0, s, out,
                        (const uint16_t *)w, (const uint16_t *)x, tokens, rows, cols, row_tiles,
                        xcd);
     return hipGetLastError() == hipSuccess;
@@ -793,6 +1043,16 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(uint16_t *__restrict__ ou
 }  // namespace
 
 namespace {
+/* f32 router logits: the reference's order on every path */
+bool launch_bf16_ref_any(float *out, const void *w, const void *x, uint32_t tokens,
+                         uint32_t rows, uint32_t cols, hipStream_t s) {
+    if (tokens == 1u) return launch_bf16_rows_ref<1>(out, w, x, 1u, rows, cols, s);
+    if (tokens <= 4u) return launch_bf16_rows_ref<4>(out, w, x, tokens, rows, cols, s);
+    if (tokens >= kGemmMinTokens && cols % 8u == 0u && ((uintptr_t)w | (uintptr_t)x) % 16u == 0u)
+        return launch_bf16_gemm_ref(out, w, x, tokens, rows, cols, s);
+    return launch_bf16_rows_ref<16>(out, w, x, tokens, rows, cols, s);
+}
+
 template <bool B16>
 bool launch_bf16_rows_any(void *out, const void *w, const void *x, uint32_t tokens,
                           uint32_t rows, uint32_t cols, hipStream_t s) {
@@ -807,7 +1067,7 @@ bool launch_bf16_rows_any(void *out, const void *w, const void *x, uint32_t toke
 
 bool k3::launch_bf16_rows_f32_any(float *out, const void *w, const void *x, uint32_t tokens,
                                   uint32_t rows, uint32_t cols, hipStream_t s) {
-    return launch_bf16_rows_any<false>(out, w, x, tokens, rows, cols, s);
+    return launch_bf16_ref_any(out, w, x, tokens, rows, cols, s);
 }
 
 bool k3::launch_bf16_rows_bf16_any(uint16_t *out, const void *w, const void *x, uint32_t tokens,
@@ -896,13 +1156,10 @@ extern "C" bool k3_rocm_bf16_gemm_tiled_f32(void *output, const void *weights,
     if (!output || !weights || !input || vector_count == 0u || vector_count > 65535u ||
         rows == 0u || columns == 0u)
         return false;
-    const hipStream_t s = (hipStream_t)stream;
-    switch (batch_tile) {
-        case 16u: return launch_bf16_rows_f32<16>(output, weights, input, vector_count, rows, columns, s);
-        case 32u: return launch_bf16_rows_f32<32>(output, weights, input, vector_count, rows, columns, s);
-        case 64u: return launch_bf16_rows_f32<64>(output, weights, input, vector_count, rows, columns, s);
-        default: return false;
-    }
+    /* the tile changes no bit of the reference's per-row order */
+    if (batch_tile != 16u && batch_tile != 32u && batch_tile != 64u) return false;
+    return k3::launch_bf16_rows_f32_any((float *)output, weights, input, vector_count, rows,
+                                        columns, (hipStream_t)stream);
 }
 
 extern "C" bool k3_rocm_bf16_gemm_f32(void *output, const void *weights, const void *input,

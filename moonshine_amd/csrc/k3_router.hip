@@ -1,8 +1,8 @@
 /*
  * Certified MFMA router for token batches (prefill). The routes and weights
- * are those of the exact router -- logits in the w64 order
- * (bf16_rows_f32_kernel / bf16_gemm_w64_kernel, k3_rocm_ops.cu:359-425,
- * 512-661) followed by router_topk_kernel (k3_rocm_ops.cu:1361-1450) -- bit
+ * are those of the exact router -- logits in the reference's own order
+ * (ref_quad / ref_chunk: k3_bf16_gemv_kernel<float> and the tiled GEMM,
+ * k3_rocm_ops.cu:359-425, 512-661) followed by router_topk_kernel (k3_rocm_ops.cu:1361-1450) -- bit
  * for bit, while the logit GEMM runs on bf16 MFMA:
  *
  *   router_norms_kernel    n_e >= ||w_e|| for every router row
@@ -12,7 +12,7 @@
  *                          router_slices_sum_kernel adds the slices)
  *   router_certify_kernel  one block per token: candidates from the
  *                          approximate logits and a rigorous error bound,
- *                          exact w64-order logits for the candidates only,
+ *                          exact reference-order logits for the candidates only,
  *                          then the exact router's top-k on exact keys
  *   router_certify_wave_kernel  the same with one wave per token, for
  *                          batches of 1024 tokens and more
@@ -25,8 +25,9 @@
  * block-aligned adder of fp32 width stays within 2 u per term; the worst
  * case measured over adversarial blocks is 8 u sum|p_block|). The H / 32
  * block results are added in fp32 (H / 32 - 1 roundings in any order),
- * and the exact w64 chain has <= 128 fmaf roundings per lane plus a
- * 6-level butterfly. The kernel uses err_e = (H / 32 + 270) u (1 + 2^-10)
+ * and in the exact reference-order sum a product passes at most 3
+ * roundings inside its quad, H / 1024 partial adds and an 8-level tree
+ * (fewer than the 128 + 6 the bound has room for up to H = 131072). The kernel uses err_e = (H / 32 + 270) u (1 + 2^-10)
  * n_e ||x_t||, which covers both sums' errors together, since sum|p_i| <=
  * ||w_e|| ||x_t|| (Cauchy-Schwarz).
  *
@@ -401,7 +402,7 @@ struct CertSmem {
 
 /*
  * One block of 4 waves per token. Wave 0 derives the candidate list from
- * the approximate logits; then every wave computes the exact w64-order
+ * the approximate logits; then every wave computes the exact reference-order
  * logits of candidates wave, wave + 4, ... (lane l takes x chunks l, l +
  * 64, ... -- the chunks it owns in that order -- from the block's copy of
  * the row in LDS, and the next candidate row's loads are issued before the
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
         if (lane == 0u) sm.ncand = ncand;
     }
     __syncthreads();
-    /* exact w64-order logits of this wave's candidates, two rows in flight */
+    /* exact reference-order logits of this wave's candidates, two rows in flight */
     const uint32_t ncand = sm.ncand;
     auto load_row = [&](uint32_t e, uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) {
         const uint32_t eu = (uint32_t)__builtin_amdgcn_readfirstlane((int)e); /* wave-uniform */
@@ -521,21 +522,12 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
         }
     };
     auto dot_row = [&](const uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) -> float {
-        float s1[1] = {0.0f};
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < kTopkSlots; j++) {
-            if (lane + 64u * (uint32_t)j < chunks) {
-                const uint4 xq = sm.x[lane + 64u * (uint32_t)j];
-                const uint32_t xu[4] = {xq.x, xq.y, xq.z, xq.w};
-                const uint32_t a[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    s1[0] = fmaf(bf16_lo(a[q]), bf16_lo(xu[q]), s1[0]);
-                    s1[0] = fmaf(bf16_hi(a[q]), bf16_hi(xu[q]), s1[0]);
-                }
-            }
-        }
-        return wave_sum_rows<1>(s1);
+        for (int j = 0; j < kTopkSlots; j++)
+            if (lane + 64u * (uint32_t)j < chunks)
+                ref_chunk(acc, j, v[j], sm.x[lane + 64u * (uint32_t)j]);
+        return ref_logit_finish(acc);
     };
     uint4 wa[kTopkSlots], wb[kTopkSlots];
     const uint32_t *cid = sm.topk.cand_id;
@@ -562,12 +554,13 @@ __global__ __launch_bounds__(256, 3) void router_certify_kernel(CertArgs A) {
  * block runs with one busy wave (candidate list, selection) no longer
  * idle three others, and twice as many tokens are in flight per CU. The
  * token's row stays in registers (lane l holds chunks l, l + 64, ..., the
- * w64 order's), the candidate rows are computed two in flight, and the
+ * chunks the reference order's ref_chunk takes), the candidate rows are
+ * computed two in flight, and the
  * selection runs on the candidates only:
  *   candidates  approximate keys, T_k by kth_largest_key, E_k, the bound
  *               lim; candidate ids and biases go to the wave's
  *               cand_id / cand_score (positions in expert order);
- *   exact       w64-order logits of the candidates (into cand_key);
+ *   exact       reference-order logits of the candidates (into cand_key);
  *   select      each candidate's exact key (router_sigmoid + bias) and
  *               weight score (det_sigmoid), compacted to keys != 0, then
  *               topk_rank_write: the exact router's ranking and weights.
@@ -676,7 +669,7 @@ __global__ __launch_bounds__(256, 2) void router_certify_wave_kernel(CertArgs A)
         const uint32_t c = lane + 64u * (uint32_t)j;
         xv[j] = c < chunks ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
     }
-    /* exact w64-order logits, two candidate rows in flight */
+    /* exact reference-order logits, two candidate rows in flight */
     auto load_row = [&](uint32_t p, uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) {
         const uint32_t eu = (uint32_t)__builtin_amdgcn_readfirstlane((int)sm.cand_id[p]);
         const uint4 *wr = (const uint4 *)(A.w + (uint64_t)eu * H);
@@ -687,24 +680,19 @@ __global__ __launch_bounds__(256, 2) void router_certify_wave_kernel(CertArgs A)
         }
     };
     auto dot_row = [&](const uint4 (&v)[kTopkSlots]) __attribute__((always_inline)) -> float {
-        float s1[1] = {0.0f};
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < kTopkSlots; j++) {
             if (lane + 64u * (uint32_t)j < chunks) {
                 /* opaque copy: keeps the row's fp32 conversions inside the
                  * loop over candidates (hoisted, they would take 128
                  * registers) */
-                uint32_t xu[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-                asm volatile("" : "+v"(xu[0]), "+v"(xu[1]), "+v"(xu[2]), "+v"(xu[3]));
-                const uint32_t a[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    s1[0] = fmaf(bf16_lo(a[q]), bf16_lo(xu[q]), s1[0]);
-                    s1[0] = fmaf(bf16_hi(a[q]), bf16_hi(xu[q]), s1[0]);
-                }
+                uint4 xu = xv[j];
+                asm volatile("" : "+v"(xu.x), "+v"(xu.y), "+v"(xu.z), "+v"(xu.w));
+                ref_chunk(acc, j, v[j], xu);
             }
         }
-        return wave_sum_rows<1>(s1);
+        return ref_logit_finish(acc);
     };
     uint4 wa[kTopkSlots], wb[kTopkSlots];
     if (ncand > 0u) load_row(0u, wa);

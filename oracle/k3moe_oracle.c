@@ -191,27 +191,39 @@ static float logit_w64(const uint16_t *w, const uint16_t *x, uint32_t h) {
     return butterfly64(lane);
 }
 
-/* Reference order, k3_rocm_ops.cu:359-425 (quad path): 256 lanes, lane j
- * sums quads j, j+256, ... as ((p0+p1)+p2)+p3 added to the partial, then the
- * LDS tree 128 -> 1. The reference is built with -ffast-math, so its own
- * bits may differ by contraction; this is for tolerance checks only. */
+/* Reference order, k3_rocm_ops.cu:359-425 (and the tiled GEMM's quad path,
+ * :512-661, which has the same per-row order): 256 lanes, lane j sums quads
+ * j, j+256, ...; then the LDS tree 128 -> 1. The reference is built with
+ * -ffast-math, so the order inside a quad is the one its compiler chose;
+ * hipcc (ROCm 7.2, gfx950) emits, for the quad expression at :381-392,
+ * v_pk_mul_f32 of (w2 x2, w3 x3), v_pk_fma_f32 giving (w1 x1 + w2 x2,
+ * w0 x0 + w3 x3), then two adds: partial + ((p1 + p2) + (p0 + p3)), each
+ * step rounded to fp32. The pair path (:395-405) adds p1 then p0; the
+ * scalar path (:407-411) is one fmaf per element. */
 static float logit_ref256(const uint16_t *w, const uint16_t *x, uint32_t h) {
     float p[256];
+#define BF(a, i) k3o_bf16_to_f32((a)[i])
     for (uint32_t t = 0; t < 256u; t++) {
         float s = 0.0f;
         if ((h & 3u) == 0u) {
             for (uint32_t q = t; q < h / 4u; q += 256u) {
                 const uint32_t i = 4u * q;
-                float a = k3o_bf16_to_f32(w[i]) * k3o_bf16_to_f32(x[i]);
-                a = a + k3o_bf16_to_f32(w[i + 1]) * k3o_bf16_to_f32(x[i + 1]);
-                a = a + k3o_bf16_to_f32(w[i + 2]) * k3o_bf16_to_f32(x[i + 2]);
-                a = a + k3o_bf16_to_f32(w[i + 3]) * k3o_bf16_to_f32(x[i + 3]);
-                s += a;
+                const float p2 = BF(w, i + 2) * BF(x, i + 2);
+                const float p3 = BF(w, i + 3) * BF(x, i + 3);
+                const float a = fmaf(BF(w, i + 1), BF(x, i + 1), p2);
+                const float b = fmaf(BF(w, i), BF(x, i), p3);
+                s = s + (a + b);
+            }
+        } else if ((h & 1u) == 0u) {
+            for (uint32_t q = t; q < h / 2u; q += 256u) {
+                const uint32_t i = 2u * q;
+                s = s + BF(w, i + 1) * BF(x, i + 1);
+                s = s + BF(w, i) * BF(x, i);
             }
         } else {
-            for (uint32_t i = t; i < h; i += 256u)
-                s += k3o_bf16_to_f32(w[i]) * k3o_bf16_to_f32(x[i]);
+            for (uint32_t i = t; i < h; i += 256u) s = fmaf(BF(w, i), BF(x, i), s);
         }
+#undef BF
         p[t] = s;
     }
     return tree_reduce(p, 256u);
@@ -363,8 +375,15 @@ static float mx_row_w64(const uint8_t *p, const uint8_t *s,
 }
 
 /* Reference order, k3_rocm_ops.cu:225-273: 128 lanes, lane j owns groups
- * j, j+128, ...; partial += dot8(x)+dot8(y)+dot8(z)+dot8(w) where each dot8
- * sums e2m1*scale*x over 8 columns; LDS tree 64 -> 1. */
+ * j, j+128, ...; LDS tree 64 -> 1. The source sums four dot8 partials of
+ * e2m1 * scale * x; under -ffast-math hipcc (ROCm 7.2, gfx950) factors the
+ * group's scale out and emits one chain over the 32 products e2m1 * x
+ * (each exact in fp32): a multiply of column 2, then fmaf in the column
+ * order of kRefGroupOrder, then partial = fmaf(chain, 2^(s-127), partial). */
+static const uint8_t kRefGroupOrder[32] = {
+    2, 1, 0, 3, 4, 5, 6, 7, 9, 8, 10, 11, 12, 13, 14, 15,
+    17, 16, 18, 19, 20, 21, 22, 23, 25, 24, 26, 27, 28, 29, 30, 31};
+
 static float mx_row_ref128(const uint8_t *p, const uint8_t *s,
                            const uint16_t *x, uint32_t cols) {
     float part[128];
@@ -372,17 +391,14 @@ static float mx_row_ref128(const uint8_t *p, const uint8_t *s,
     for (uint32_t t = 0; t < 128u; t++) {
         float acc = 0.0f;
         for (uint32_t g = t; g < groups; g += 128u) {
-            const float sc = k3o_e8m0(s[g]);
-            float d[4];
-            for (uint32_t q = 0; q < 4u; q++) {
-                float pd = 0.0f;
-                for (uint32_t i = 0; i < 8u; i++) {
-                    const uint32_t c = 32u * g + 8u * q + i;
-                    pd += nib(p, c) * sc * k3o_bf16_to_f32(x[c]);
-                }
-                d[q] = pd;
+            const uint32_t c0 = 32u * g;
+            uint32_t c = c0 + kRefGroupOrder[0];
+            float ch = nib(p, c) * k3o_bf16_to_f32(x[c]);
+            for (uint32_t i = 1; i < 32u; i++) {
+                c = c0 + kRefGroupOrder[i];
+                ch = fmaf(nib(p, c), k3o_bf16_to_f32(x[c]), ch);
             }
-            acc += ((d[0] + d[1]) + d[2]) + d[3];
+            acc = fmaf(ch, k3o_e8m0(s[g]), acc);
         }
         part[t] = acc;
     }
@@ -787,8 +803,9 @@ int k3o_layer(const k3o_shape *sh, uint32_t tokens,
             memcpy(ids + (uint64_t)i * K, ids_in + (uint64_t)t * K, 4u * K);
             memcpy(wts + (uint64_t)i * K, weights_in + (uint64_t)t * K, 4u * K);
         } else {
-            k3o_bf16_gemm_f32(logits + (uint64_t)i * E, router_weight, x, 1u, E, H,
-                              gemv_order == 1 ? 1 : 0);
+            /* the router's logits in the reference's order (every router
+             * path of the library computes them that way) */
+            k3o_bf16_gemm_f32(logits + (uint64_t)i * E, router_weight, x, 1u, E, H, 1);
             k3o_router_topk(ids + (uint64_t)i * K, wts + (uint64_t)i * K,
                             logits + (uint64_t)i * E, router_bias, 1u, E, K,
                             sh->scale, 0);

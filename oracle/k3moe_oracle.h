@@ -133,7 +133,9 @@ typedef struct {
  * the router (lets a test check the expert stage on the GPU's own routes).
  * experts[e] may be NULL for experts that are never selected.
  * expert_out (optional) receives [tokens, top_k, hidden] bf16 slot outputs.
- * gemv_order: 0 = w64, 1 = reference lane order, 2 = fp64, 3 = MX8 (the
+ * The router's logits are always in the reference's lane order.
+ * gemv_order (the expert GEMVs): 0 = w64, 1 = reference lane order, 2 =
+ * fp64, 3 = MX8 (the
  * expert inputs -- x for gate/up, the activation for down -- quantized to
  * MXFP8, products accumulated in fp64; same bf16 rounding points as the
  * other orders), 4 = split MX8 (inputs as the two-term hi + lo

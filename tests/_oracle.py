@@ -90,7 +90,9 @@ def _ptr(a):
     return None if a is None else a.ctypes.data_as(_p)
 
 
-def router_logits(w, x, order=ORDER_W64):
+def router_logits(w, x, order=ORDER_REF):
+    """Router logits; by default in the reference's order, which every
+    router path of the library computes (k3_rocm_ops.cu:359-425)."""
     E, H = w.shape
     T = x.shape[0]
     out = np.empty((T, E), np.float32)
@@ -132,7 +134,7 @@ def route_weights(ids, logits, scale):
     return out
 
 
-def check_routes(got_ids, got_w, logits, bias, k, scale):
+def check_routes(got_ids, got_w, logits, bias, k, scale, max_bad=None):
     """Device routes against the oracle router on the same logits.
 
     The device orders experts by the hardware sigmoid the reference kernel
@@ -143,9 +145,14 @@ def check_routes(got_ids, got_w, logits, bias, k, scale):
     ids differ must hold a top-k of the oracle's choices when each choice may
     be off by 4 ulp of the sigmoid plus one rounding of the bias add.
     Weights are bit-exact to the oracle's formula on the device's own ids.
+    At most max_bad tokens (default max(1, T // 1000)) may differ, so a
+    change that moves many tokens onto near-tie alternatives fails.
     Returns the indices of the tokens whose ids differ."""
     want_ids, want_w = router_topk(logits, bias, k, scale)
     bad = np.nonzero((np.asarray(got_ids) != want_ids).any(axis=1))[0]
+    T = np.asarray(got_ids).shape[0]
+    limit = max(1, T // 1000) if max_bad is None else max_bad
+    assert bad.size <= limit, f"{bad.size} of {T} tokens route differently from the oracle"
     for t in bad:
         c = router_choices(logits[t], bias).astype(np.float64)
         tol = 4 * 2.0 ** -24 + 2.0 ** -23 * np.abs(c)
@@ -185,7 +192,7 @@ def mxfp4_gemm(packed, scales, x, rows, cols, order=ORDER_W64):
     return out, f
 
 
-def bf16_gemm_f32(w, x, order=ORDER_W64):
+def bf16_gemm_f32(w, x, order=ORDER_REF):
     rows, cols = w.shape
     T = x.shape[0]
     out = np.empty((T, rows), np.float32)
@@ -194,7 +201,8 @@ def bf16_gemm_f32(w, x, order=ORDER_W64):
 
 
 def bf16_gemm_bf16(w, x, order=ORDER_W64):
-    """bf16 output of the bf16 -> f32 order, rounded once."""
+    """bf16 output of the bf16 -> f32 sum (the library's bf16 projections
+    use the w64 order), rounded once."""
     from moonshine_amd.synth import f32_to_bf16_bits
     return f32_to_bf16_bits(bf16_gemm_f32(w, x, order))
 

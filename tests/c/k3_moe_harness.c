@@ -203,7 +203,7 @@ int main(void) {
         float *logits = malloc(4 * (size_t)T * E);
         CHECK(hipMemcpy(got_ids, d_rids, sizeof got_ids, hipMemcpyDeviceToHost) == hipSuccess);
         CHECK(hipMemcpy(got_w, d_rw, sizeof got_w, hipMemcpyDeviceToHost) == hipSuccess);
-        k3o_router_logits(logits, router_w, xb, T, E, H, 0);
+        k3o_router_logits(logits, router_w, xb, T, E, H, 1); /* the reference order */
         CHECK(k3o_router_topk(want_ids, want_w, logits, bias, T, E, K, 2.5f, 0) == 0);
         const int rb = memcmp(got_ids, want_ids, sizeof got_ids) != 0 ||
                        memcmp(got_w, want_w, sizeof got_w) != 0;

@@ -1,8 +1,9 @@
 """GPU parity of the fused routed-MoE layer (k3_moe_forward_bf16) against the
 CPU oracle on the seeded benchmark configurations.
 
-Exact precision is bit-identical to the oracle's w64 order: logits, expert
-ids, route weights, the routing plan and the layer output.
+Exact precision is bit-identical to the oracle: router logits (the
+reference's own order), expert ids, route weights, the routing plan and the
+layer output (expert GEMVs in the w64 order).
 """
 import ctypes
 
@@ -107,7 +108,7 @@ def test_decode_layer_bitexact(cuda, cfg):
     moe = get_layer(cfg, inputs, cuda)
     out, ids, w = run(cfg, inputs, moe, cuda)
     want = O.layer(cfg, inputs, host_experts(moe.store, ids))
-    # logits bit-exact too (fixed w64 order)
+    # logits bit-exact too (the reference's order)
     logits = torch.zeros((1, cfg.experts), dtype=torch.float32, device=cuda)
     from moonshine_amd import ops
     assert ops.k3_rocm_bf16_gemv_f32(logits, moe.router_weight, L.bf16_tensor(inputs.hidden, cuda),
