@@ -169,6 +169,29 @@ bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
                          size_t workspace_bytes, void *stream);
 
 /*
+ * k3_moe_forward_bf16 for a layer whose router reads another input than its
+ * experts: the K3 engine's form, where the router runs on the post-norm
+ * hidden state [T, router_columns] (k3_engine.cu:1554-1557,
+ * k3_engine_prefill.inc:1448-1453) and the experts on the latent [T,
+ * shape->hidden] produced by routed_expert_down_proj (k3_engine.cu:1668-1672).
+ * output [T, shape->hidden] = bf16(residual + bf16(sum_r w_r y_r)), or the
+ * combine alone when residual is NULL (the engine's routed_up projection
+ * follows it). No reference counterpart: it replaces the router, top-k,
+ * host sync, expert loop and weighted sum of decode_routed_layer and
+ * prefill_routed_layer. router_columns % 8 == 0 (<= 8192 for one token);
+ * router_input and router_weight 16-byte aligned; workspace
+ * k3_moe_workspace_bytes(shape, T) (the router's width does not change it).
+ * Routes, workspace and alignment otherwise as k3_moe_forward_bf16.
+ */
+bool k3_moe_routed_bf16(void *output, const void *router_input, uint32_t router_columns,
+                        const void *expert_input, const void *residual,
+                        const void *router_weight, const void *router_bias,
+                        const k3_moe_expert *experts, const k3_moe_shape *shape,
+                        uint32_t token_count, uint32_t precision, void *expert_ids,
+                        void *expert_weights, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/*
  * k3_moe_forward_bf16 without a caller workspace, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). No counterpart in the
@@ -180,7 +203,11 @@ bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
  * E 896, k 16, F 2048) up to 64 tokens fit. The call allocates nothing.
  * Every call on one GPU shares that GPU's array: calls that may overlap
  * on one GPU (two streams, two host threads) race and must be serialised
- * by the caller. Arguments otherwise as k3_moe_forward_bf16.
+ * by the caller. The array belongs to the library's code object, so each
+ * GPU where the library is loaded holds it even if this entry point is
+ * never called; its address is cached per device, so a process that calls
+ * this entry point must not hipDeviceReset that device afterwards.
+ * Arguments otherwise as k3_moe_forward_bf16.
  */
 #define K3_MOE_STATIC_WORKSPACE_BYTES (32u << 20)
 bool k3_moe_forward_static_bf16(void *output, const void *hidden, const void *residual,

@@ -119,6 +119,8 @@ SIGNATURES = {
                                           _u32, _u32, _p, _p, _p, _sz, _p, _p]),
     "k3_moe_forward_static_bf16": (_b, [_p, _p, _p, _p, _p, _p, ctypes.POINTER(K3MoeShape),
                                         _u32, _u32, _p, _p, _p]),
+    "k3_moe_routed_bf16": (_b, [_p, _p, _u32, _p, _p, _p, _p, _p, ctypes.POINTER(K3MoeShape),
+                                _u32, _u32, _p, _p, _p, _sz, _p]),
     "k3_moe_router_choices_f32": (_b, [_p, _p, _p, _u32, _u32, _p]),
     "k3_moe_experts_bf16": (_b, [_p, _p, _p, _p, _p, _p, ctypes.POINTER(K3MoeShape), _u32,
                                  _u32, _p, _sz, _p]),

@@ -789,6 +789,40 @@ extern "C" bool k3_moe_forward_profiled_bf16(void *output, const void *hidden, c
                        mark);
 }
 
+extern "C" bool k3_moe_routed_bf16(void *output, const void *router_input,
+                                   uint32_t router_columns, const void *expert_input,
+                                   const void *residual, const void *router_weight,
+                                   const void *router_bias, const k3_moe_expert *experts,
+                                   const k3_moe_shape *shape, uint32_t token_count,
+                                   uint32_t precision, void *expert_ids, void *expert_weights,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+    if (!output || !router_input || !expert_input || !router_weight || !router_bias ||
+        !experts || !workspace || router_columns == 0u ||
+        !precision_ok(shape, token_count, precision) ||
+        !rows_aligned(output, expert_input, residual) ||
+        (((uintptr_t)router_input | (uintptr_t)router_weight) % 16u) != 0u ||
+        router_columns % 8u != 0u)
+        return false;
+    Workspace ws = carve(workspace, *shape, token_count);
+    if (workspace_bytes < ws.bytes) return false;
+    const hipStream_t st = (hipStream_t)stream;
+    const StageMarker mark{nullptr, st};
+    if (token_count == 1u && decode_supported(*shape) && router_columns <= 8192u) {
+        DecodeParams P = decode_params(ws, output, expert_input, residual, router_weight,
+                                       router_bias, experts, *shape, expert_ids, expert_weights);
+        P.router_in = (const uint16_t *)router_input;
+        P.router_cols = router_columns;
+        return decode_launch(P, st, mark);
+    }
+    k3_moe_shape rs = *shape; /* the router's width */
+    rs.hidden = router_columns;
+    if (!route_batch(ws, router_input, router_weight, router_bias, rs, token_count, expert_ids,
+                     expert_weights, st, &mark))
+        return false;
+    return run_experts(ws, output, expert_input, residual, experts, *shape, token_count,
+                       precision, st, mark);
+}
+
 bool k3::native_decode_experts(void *routed_out, const void *x, uint32_t router_cols,
                            const void *latent, const void *router_weight,
                            const void *router_bias, const k3_moe_expert *experts,

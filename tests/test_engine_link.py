@@ -31,7 +31,7 @@ def nm(path, *flags):
 def built():
     r = subprocess.run(["make", "-j8", "-C", str(D)], capture_output=True, text=True)
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
-    return B / "libk3engine_on_k3moe.so"
+    return D / "lib" / "libk3engine_on_k3moe.so"
 
 
 def test_headers_declare_the_reference_signatures(built):
