@@ -1,13 +1,14 @@
-"""Python mirror of the routed-MoE entry points of Moonshine's k3_rocm_ops.h.
+"""Test helper: the per-matrix entry points of include/k3_rocm_ops.h
+(k3_rocm_ops.h of the reference) called on torch device tensors.
 
 Each function keeps the reference's name, argument order and meaning and
 returns the C launcher's bool (False = invalid arguments, nothing launched).
-Tensors are torch device tensors; `stream` defaults to torch's current
-stream. Everything runs in libk3moe.so (gfx950 HIP); there is no other path.
+`stream` defaults to torch's current stream. Everything runs in
+libk3moe.so (gfx950 HIP); there is no other path.
 """
 import ctypes
 
-from ._lib import lib
+from moonshine_amd._lib import lib
 
 
 def _ptr(t):

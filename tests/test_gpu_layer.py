@@ -110,7 +110,7 @@ def test_decode_layer_bitexact(cuda, cfg):
     want = O.layer(cfg, inputs, host_experts(moe.store, ids))
     # logits bit-exact too (the reference's order)
     logits = torch.zeros((1, cfg.experts), dtype=torch.float32, device=cuda)
-    from moonshine_amd import ops
+    import _ops as ops
     assert ops.k3_rocm_bf16_gemv_f32(logits, moe.router_weight, L.bf16_tensor(inputs.hidden, cuda),
                                      cfg.experts, cfg.hidden)
     torch.cuda.synchronize()
@@ -411,7 +411,7 @@ def test_routes_into_mapped_host_memory(cuda, T):
         np.testing.assert_array_equal(mw.array(np.float32, n).reshape(T, -1), want["weights"])
         np.testing.assert_array_equal(L.bf16_bits(out), want["output"])
         # the single-vector router ABI into the same mapped buffers
-        from moonshine_amd import ops
+        import _ops as ops
         logits = torch.from_numpy(O.router_logits(inputs.router_weight, inputs.hidden)[0]).to(cuda)
         mi.array(np.uint32, n)[:] = 0
         assert ops.lib().k3_rocm_router_topk_f32(mi.dev, mw.dev, P(logits), P(moe.router_bias),

@@ -199,7 +199,7 @@ def test_proj_mfma_ragged_vs_row_kernels(cuda, q8, T, rows, cols):
     plus one bf16 rounding step of the larger value; most elements are
     identical."""
     import ctypes
-    from moonshine_amd import ops
+    import _ops as ops
     from moonshine_amd._lib import lib
     rng = np.random.default_rng(T * 1000 + rows + cols + q8)
     x = f32_to_bf16_bits(rng.normal(0, 1, (T, cols)).astype(np.float32))

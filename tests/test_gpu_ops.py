@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import _oracle as O
-from moonshine_amd import ops
+import _ops as ops
 from moonshine_amd.synth import bf16_bits_to_f32, f32_to_bf16_bits
 
 pytestmark = pytest.mark.gpu

@@ -39,7 +39,7 @@ import torch
 
 import _oracle as O
 from moonshine_amd import layer as L
-from moonshine_amd import ops
+import _ops as ops
 from moonshine_amd._lib import SIGNATURES
 from moonshine_amd.synth import ACT_SITU, CONFIGS, K3_NATIVE, bf16_bits_to_f32, make_inputs
 

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from moonshine_amd import ops
+import _ops as ops
 from moonshine_amd._lib import lib
 from moonshine_amd.synth import CONFIGS, f32_to_bf16_bits, make_inputs
 

@@ -28,7 +28,7 @@ import torch
 
 import _oracle as O
 from moonshine_amd import layer as L
-from moonshine_amd import ops
+import _ops as ops
 from moonshine_amd._lib import SIGNATURES
 from moonshine_amd.synth import CONFIGS, EXACT, MFMA, make_inputs
 
