@@ -8,6 +8,8 @@
 
 namespace k3 {
 
+struct RouterRows; /* k3_topk.h */
+
 struct DecodeParams {
     uint16_t *output;
     const uint16_t *residual;
@@ -48,6 +50,8 @@ bool decode_supported(const k3_moe_shape &s);
 bool decode_launch(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
 /* router and top-k only (decode_launch's first half) */
 bool decode_launch_route(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
+/* top-k only, on router outputs already in p.logits / p.scores / p.keys */
+bool decode_launch_topk(const DecodeParams &p, hipStream_t stream, const StageMarker &mark);
 /* gate/up, down, combine on routes in p.ids / p.weights (resolve: look the
  * expert descriptors up first, for routes that did not come from
  * decode_launch's top-k) */
@@ -60,11 +64,23 @@ bool decode_launch_experts(const DecodeParams &p, hipStream_t stream, const Stag
  * workspace is the routed layer's (k3_moe_workspace_bytes(shape, 1)).
  * With latent_ready, the experts wait for that event (the latent may be
  * produced on another stream) while router and top-k do not. */
+/* With `routed`, the router outputs are already in the workspace (filled
+ * through native_decode_router_rows) and only top-k runs before the
+ * experts. */
 bool native_decode_experts(void *routed_out, const void *x, uint32_t router_cols,
                            const void *latent, const void *router_weight,
                            const void *router_bias, const k3_moe_expert *experts,
                            const k3_moe_shape &shape, void *ids_copy, void *w_copy,
                            void *workspace, size_t workspace_bytes, hipEvent_t latent_ready,
-                           hipStream_t stream);
+                           bool routed, hipStream_t stream);
+
+/* The router rows native_decode_experts computes (x, weights and where in
+ * the workspace the logits, scores and keys go), for a caller that fuses
+ * them into another launch. False when native_decode_experts would reject
+ * the arguments. */
+bool native_decode_router_rows(RouterRows *out, const void *x, uint32_t router_cols,
+                               const void *router_weight, const void *router_bias,
+                               const k3_moe_shape &shape, void *workspace,
+                               size_t workspace_bytes);
 
 }  // namespace k3

@@ -44,7 +44,6 @@
 namespace k3 {
 namespace {
 
-constexpr int kRouterMaxChunks = 16;  /* hidden <= 8192 */
 constexpr int kGU = 8;                /* gate (and up) rows per gate/up block */
 /* rows per down wave (F <= 2048): 8 gives 3584 blocks for the K3 shape,
  * enough for an even tail (16 rows: 1.75 rounds of resident blocks, ~1.5
@@ -55,46 +54,14 @@ constexpr int kDownRows = 8;
 /* router                                                                  */
 /* ---------------------------------------------------------------------- */
 
-/* One wave per block computes rows 2b and 2b+1 in the reference's order
- * (ref_chunk: 16-byte chunks l, l+64, ... per lane, the reference's 256
- * partials four per lane, then its tree). Both weight rows and the hidden
- * state are loaded in one batch (one memory round trip), and the hidden
- * state is read once for the two rows: a CU's L2 read bandwidth, not HBM,
- * bounds this kernel, so rereading x per row would cost as much as a third
- * of the weights. */
+/* One wave per block computes rows 2b and 2b+1 (router_rows_wave): the
+ * hidden state is read once for the two rows, since a CU's L2 read
+ * bandwidth, not HBM, bounds this kernel and rereading x per row would
+ * cost as much as a third of the weights. */
 __global__ __launch_bounds__(64) void router_kernel(DecodeParams P) {
-    const uint32_t lane = threadIdx.x;
-    const uint32_t chunks = P.router_cols / 8u;
-    const uint32_t row0 = 2u * blockIdx.x;
-    const bool two = row0 + 1u < P.expert_count;
-    const uint4 *w0 = (const uint4 *)(P.router_weight + (uint64_t)row0 * P.router_cols);
-    const uint4 *w1 = two ? w0 + chunks : w0;
-    const uint4 *x4 = (const uint4 *)P.router_in;
-    uint4 wa[kRouterMaxChunks], wb[kRouterMaxChunks], xv[kRouterMaxChunks];
-#pragma unroll
-    for (int j = 0; j < kRouterMaxChunks; j++) {
-        /* out-of-range chunks load chunk 0 and are skipped below */
-        const uint32_t c = lane + 64u * j < chunks ? lane + 64u * j : 0u;
-        wa[j] = gload_nt(w0 + c);
-        wb[j] = gload_nt(w1 + c);
-        xv[j] = x4[c];
-    }
-    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < kRouterMaxChunks; j++) {
-        if (lane + 64u * j < chunks) {
-            ref_chunk(a, j, wa[j], xv[j]);
-            ref_chunk(b, j, wb[j], xv[j]);
-        }
-    }
-    const float va = ref_logit_finish(a), vb = ref_logit_finish(b);
-    if (lane < (two ? 2u : 1u)) {
-        const uint32_t row = row0 + lane;
-        const float v = lane ? vb : va;
-        P.logits[row] = v;
-        P.scores[row] = det_sigmoid(v);
-        P.keys[row] = choice_key(router_sigmoid(v), P.router_bias[row]);
-    }
+    const RouterRows R{P.router_weight, P.router_bias, P.router_in, P.logits,
+                       P.scores,        P.keys,        P.expert_count, P.router_cols};
+    router_rows_wave<2>(R, 2u * blockIdx.x);
 }
 
 /* Lane s < top_k stores the descriptor of route s (id `e`) and the wave
@@ -419,6 +386,10 @@ bool decode_supported(const k3_moe_shape &s) {
 bool decode_launch_route(const DecodeParams &P, hipStream_t st, const StageMarker &mark) {
     mark(K3_MOE_STAGE_ROUTER);
     hipLaunchKernelGGL(router_kernel, dim3((P.expert_count + 1u) / 2u), dim3(64), 0, st, P);
+    return hipGetLastError() == hipSuccess && decode_launch_topk(P, st, mark);
+}
+
+bool decode_launch_topk(const DecodeParams &P, hipStream_t st, const StageMarker &mark) {
     mark(K3_MOE_STAGE_TOPK);
     hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(64), 0, st, P);
     return hipGetLastError() == hipSuccess;

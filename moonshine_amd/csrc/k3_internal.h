@@ -6,6 +6,8 @@
 
 namespace k3 {
 
+struct RouterRows; /* k3_topk.h */
+
 /* f32 [tokens, rows] = bf16 weights [rows, cols] . bf16 input [tokens, cols]
  * in the w64 order. */
 bool launch_bf16_rows_f32_any(float *out, const void *weights, const void *input,
@@ -53,12 +55,14 @@ bool launch_router_certified(uint32_t *ids, float *weights, uint32_t *ids2, floa
                              const StageMarker *mark);
 
 /* launch_q8_gateup (rows x cols) and launch_q8_gemv (out_rows x cols, no
- * addends) on the same x as one launch; the same bits as the two calls. */
+ * addends) on the same x as one launch; the same bits as the two calls.
+ * With `router` (its x and cols those of the projections), the same launch
+ * also writes the router's logits, scores and keys (router_rows_wave). */
 bool launch_q8_gateup_and_gemv(uint16_t *act, const void *gate_codes, const void *gate_scales,
                                const void *up_codes, const void *up_scales, const void *x,
                                uint32_t rows, uint32_t cols, uint32_t kind, float beta, float lb,
                                uint16_t *out, const void *codes, const void *scales,
-                               uint32_t out_rows, hipStream_t stream);
+                               uint32_t out_rows, const RouterRows *router, hipStream_t stream);
 
 /* Static projection of a token batch on bf16 MFMA (k3_proj.hip), for the
  * MXFP8 precisions: out [T, N] bf16 = w [N, K] . x [T, K], w Q8-128 codes

@@ -24,6 +24,7 @@
 #include "k3_internal.h"
 #include "k3_decode.h"
 #include "k3_mfma.h"
+#include "k3_topk.h"
 #include "../../include/k3_moe.h"
 #include "../../include/k3_rocm_ops.h"
 
@@ -823,15 +824,36 @@ extern "C" bool k3_moe_routed_bf16(void *output, const void *router_input,
                        precision, st, mark);
 }
 
+namespace {
+
+bool native_decode_args_ok(const void *x, uint32_t router_cols, const void *router_weight,
+                           const k3_moe_shape &shape) {
+    return k3::decode_supported(shape) && router_cols != 0u && router_cols % 8u == 0u &&
+           router_cols <= 8192u && (((uintptr_t)x | (uintptr_t)router_weight) % 16u) == 0u;
+}
+
+}  // namespace
+
+bool k3::native_decode_router_rows(RouterRows *out, const void *x, uint32_t router_cols,
+                                   const void *router_weight, const void *router_bias,
+                                   const k3_moe_shape &shape, void *workspace,
+                                   size_t workspace_bytes) {
+    if (!native_decode_args_ok(x, router_cols, router_weight, shape)) return false;
+    const Workspace ws = carve(workspace, shape, 1u);
+    if (workspace_bytes < ws.bytes) return false;
+    *out = RouterRows{(const uint16_t *)router_weight, (const float *)router_bias,
+                      (const uint16_t *)x, ws.logits, ws.scores, ws.keys, shape.expert_count,
+                      router_cols};
+    return true;
+}
+
 bool k3::native_decode_experts(void *routed_out, const void *x, uint32_t router_cols,
-                           const void *latent, const void *router_weight,
-                           const void *router_bias, const k3_moe_expert *experts,
-                           const k3_moe_shape &shape, void *ids_copy, void *w_copy,
-                           void *workspace, size_t workspace_bytes, hipEvent_t latent_ready,
-                           hipStream_t st) {
-    if (!decode_supported(shape) || router_cols == 0u || router_cols % 8u != 0u ||
-        router_cols > 8192u || (((uintptr_t)x | (uintptr_t)router_weight) % 16u) != 0u)
-        return false;
+                               const void *latent, const void *router_weight,
+                               const void *router_bias, const k3_moe_expert *experts,
+                               const k3_moe_shape &shape, void *ids_copy, void *w_copy,
+                               void *workspace, size_t workspace_bytes, hipEvent_t latent_ready,
+                               bool routed, hipStream_t st) {
+    if (!native_decode_args_ok(x, router_cols, router_weight, shape)) return false;
     Workspace ws = carve(workspace, shape, 1u);
     if (workspace_bytes < ws.bytes) return false;
     DecodeParams P = decode_params(ws, routed_out, latent, nullptr, router_weight, router_bias,
@@ -839,7 +861,8 @@ bool k3::native_decode_experts(void *routed_out, const void *x, uint32_t router_
     P.router_in = (const uint16_t *)x;
     P.router_cols = router_cols;
     const StageMarker mark{nullptr, st};
-    if (!decode_launch_route(P, st, mark)) return false;
+    if (!(routed ? decode_launch_topk(P, st, mark) : decode_launch_route(P, st, mark)))
+        return false;
     if (latent_ready && hipStreamWaitEvent(st, latent_ready, 0) != hipSuccess) return false;
     return decode_launch_experts(P, st, mark, false);
 }

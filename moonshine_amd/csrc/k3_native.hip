@@ -12,6 +12,7 @@
 #include "../../include/k3_rocm_ops.h"
 #include "k3_decode.h"
 #include "k3_internal.h"
+#include "k3_topk.h"
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -180,6 +181,16 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
      * shared gate/up read the same x, so they run as one grid */
     const bool pair = fused && !ev && W.routed_down.kind == K3_MOE_STATIC_Q8_128 &&
                       k3::q8_gemv_fits(H, W.routed_down.data, hidden);
+    const bool decode = T == 1u && k3::decode_supported(s.routed) && H % 8u == 0u &&
+                        H <= 8192u &&
+                        (((uintptr_t)hidden | (uintptr_t)W.router_weight) % 16u) == 0u;
+    /* one-token routes with the pair grid: the router rows join that
+     * launch (they read the same x) and only top-k runs after it */
+    k3::RouterRows router{};
+    const bool router_in_pair =
+        pair && decode &&
+        k3::native_decode_router_rows(&router, hidden, H, W.router_weight, W.router_bias,
+                                      s.routed, ws.experts, ws.expert_bytes);
     /* side stream (or the main one): latent, then the shared activation */
     if (pair) {
         ok = ok && k3::launch_q8_gateup_and_gemv(ws.act, W.shared_gate.data,
@@ -187,7 +198,7 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
                                                  W.shared_up.scales, hidden, S, H,
                                                  s.routed.activation, beta, lb, ws.latent,
                                                  W.routed_down.data, W.routed_down.scales, D,
-                                                 st);
+                                                 router_in_pair ? &router : nullptr, st);
     } else {
         ok = ok && project(W.routed_down, ws.latent, hidden, T, precision, side);
     }
@@ -207,15 +218,12 @@ extern "C" bool k3_moe_native_forward_bf16(void *output, const void *hidden, con
     }
     if (ev) ok = ok && hipEventRecord(ev->act, side) == hipSuccess;
     /* main stream: routes, experts on the latent, norm, up projection */
-    const bool decode = T == 1u && k3::decode_supported(s.routed) && H % 8u == 0u &&
-                        H <= 8192u &&
-                        (((uintptr_t)hidden | (uintptr_t)W.router_weight) % 16u) == 0u;
     bool routes_copied = false;
     if (decode) {
         ok = ok && k3::native_decode_experts(ws.routed, hidden, H, ws.latent, W.router_weight,
                                              W.router_bias, W.experts, s.routed, expert_ids,
                                              expert_weights, ws.experts, ws.expert_bytes,
-                                             ev ? ev->latent : nullptr, st);
+                                             ev ? ev->latent : nullptr, router_in_pair, st);
         routes_copied = true;
     } else {
         /* token batches: the certified MFMA router (same routes) */

@@ -888,17 +888,30 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(Q8GemvArgs A) {
 
 /* Two independent single-vector projections as one grid: blocks [0, nd)
  * run the fused gate/up/activation (DUAL, 8 rows), the rest a plain
- * projection (4 rows). One launch ramp and tail instead of two. */
+ * projection (4 rows). One launch ramp and tail instead of two. With nr >
+ * 0, blocks [0, nr) first compute router rows on the same x
+ * (router_rows_wave, kPairRouterRows per wave): their latency-bound loads
+ * then overlap the projections' streaming instead of running as a launch
+ * of their own. */
+constexpr int kPairRouterRows = 1;
+
 __global__ __launch_bounds__(256) void q8_gemv_pair_kernel(Q8GemvArgs D, Q8GemvArgs S,
-                                                           uint32_t nd) {
+                                                           RouterRows R, uint32_t nd,
+                                                           uint32_t nr) {
     __shared__ union {
         Q8GemvSmem<true, 8, 1, false> d;
         Q8GemvSmem<false, 4, 1, false> s;
     } sm;
-    if (blockIdx.x < nd)
-        q8_gemv_block<true, 8, 1, false>(sm.d, blockIdx.x, D);
+    if (blockIdx.x < nr) {
+        router_rows_wave<kPairRouterRows>(
+            R, (blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * kPairRouterRows);
+        return;
+    }
+    const uint32_t b = blockIdx.x - nr;
+    if (b < nd)
+        q8_gemv_block<true, 8, 1, false>(sm.d, b, D);
     else
-        q8_gemv_block<false, 4, 1, false>(sm.s, blockIdx.x - nd, S);
+        q8_gemv_block<false, 4, 1, false>(sm.s, b - nd, S);
 }
 
 /* One wave per 128-element block: scale = max|w| / 127 (1 for an all-zero
@@ -1453,10 +1466,21 @@ bool k3::launch_q8_gateup_and_gemv(uint16_t *act, const void *gate_codes,
                                    const void *up_scales, const void *x, uint32_t rows,
                                    uint32_t cols, uint32_t kind, float beta, float lb,
                                    uint16_t *out, const void *codes, const void *scales,
-                                   uint32_t out_rows, hipStream_t st) {
+                                   uint32_t out_rows, const RouterRows *router,
+                                   hipStream_t st) {
     if (!q8_gemv_fits(cols, gate_codes, x) || !q8_gemv_fits(cols, up_codes, x) ||
         !q8_gemv_fits(cols, codes, x) || rows == 0u || out_rows == 0u)
         return false;
+    RouterRows R{};
+    uint32_t nr = 0u;
+    if (router) {
+        R = *router;
+        if (R.x != x || R.cols != cols || R.cols % 8u != 0u || R.cols > 8u * 64u * kRouterMaxChunks ||
+            ((uintptr_t)R.weight % 16u) != 0u || R.rows == 0u)
+            return false;
+        constexpr uint32_t per_block = kWavesPerBlock * kPairRouterRows;
+        nr = (R.rows + per_block - 1u) / per_block;
+    }
     const uint32_t a16d = (((uintptr_t)gate_codes | (uintptr_t)up_codes) % 16u) == 0u;
     const uint32_t a16s = ((uintptr_t)codes % 16u) == 0u;
     const Q8GemvArgs D{act, (const int8_t *)gate_codes, (const float *)gate_scales,
@@ -1466,6 +1490,7 @@ bool k3::launch_q8_gateup_and_gemv(uint16_t *act, const void *gate_codes,
                        (const uint16_t *)x, out_rows, cols, a16s, nullptr, nullptr, 0u, 1.0f,
                        1.0f, nullptr, 0.0f};
     const uint32_t nd = (rows + kQ8DualRows - 1u) / kQ8DualRows, ns = (out_rows + 3u) / 4u;
-    hipLaunchKernelGGL(q8_gemv_pair_kernel, dim3(nd + ns), dim3(256), 0, st, D, S, nd);
+    hipLaunchKernelGGL(q8_gemv_pair_kernel, dim3(nr + nd + ns), dim3(256), 0, st, D, S, R, nd,
+                       nr);
     return hipGetLastError() == hipSuccess;
 }

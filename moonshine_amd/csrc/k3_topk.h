@@ -209,4 +209,64 @@ __device__ __forceinline__ uint32_t topk_rank_write(uint32_t ncand, uint32_t top
     return id;
 }
 
+/* One token's router outputs for the top-k: per expert row, the logit
+ * (bf16 weight row . bf16 x in the reference's order, ref_chunk /
+ * ref_logit_finish), the score det_sigmoid(logit) and the order key
+ * choice_key(router_sigmoid(logit), bias) (k3_rocm_ops.cu:1361-1450). */
+struct RouterRows {
+    const uint16_t *weight; /* [rows, cols] bf16 */
+    const float *bias;      /* [rows] */
+    const uint16_t *x;      /* [cols] bf16, 16-byte aligned */
+    float *logits, *scores;
+    uint32_t *keys;
+    uint32_t rows, cols;    /* cols % 8 == 0, cols <= 8192 */
+};
+
+constexpr int kRouterMaxChunks = 16; /* cols <= 8192 */
+
+/* Rows row0 .. row0 + N - 1 (those below R.rows) on one wave. Every weight
+ * chunk and the hidden state are loaded in one batch (one memory round
+ * trip), and x is read once for the N rows. */
+template <int N>
+__device__ __forceinline__ void router_rows_wave(const RouterRows &R, uint32_t row0) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t chunks = R.cols / 8u;
+    const uint4 *x4 = (const uint4 *)R.x;
+    const uint4 *w[N];
+#pragma unroll
+    for (int r = 0; r < N; r++) /* rows past the end reread row0 (not stored) */
+        w[r] = (const uint4 *)(R.weight + (uint64_t)(row0 + r < R.rows ? row0 + r : row0) * R.cols);
+    uint4 wv[N][kRouterMaxChunks], xv[kRouterMaxChunks];
+#pragma unroll
+    for (int j = 0; j < kRouterMaxChunks; j++) {
+        /* out-of-range chunks load chunk 0 and are skipped below */
+        const uint32_t c = lane + 64u * j < chunks ? lane + 64u * j : 0u;
+#pragma unroll
+        for (int r = 0; r < N; r++) wv[r][j] = gload_nt(w[r] + c);
+        xv[j] = x4[c];
+    }
+    float acc[N][4];
+#pragma unroll
+    for (int r = 0; r < N; r++) acc[r][0] = acc[r][1] = acc[r][2] = acc[r][3] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxChunks; j++) {
+        if (lane + 64u * j < chunks) {
+#pragma unroll
+            for (int r = 0; r < N; r++) ref_chunk(acc[r], j, wv[r][j], xv[j]);
+        }
+    }
+    float v = 0.0f;
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+        const float l = ref_logit_finish(acc[r]);
+        if (lane == (uint32_t)r) v = l;
+    }
+    const uint32_t row = row0 + lane;
+    if (lane < (uint32_t)N && row < R.rows) {
+        R.logits[row] = v;
+        R.scores[row] = det_sigmoid(v);
+        R.keys[row] = choice_key(router_sigmoid(v), R.bias[row]);
+    }
+}
+
 }  // namespace k3
