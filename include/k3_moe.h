@@ -178,7 +178,8 @@ bool k3_moe_forward_bf16(void *output, const void *hidden, const void *residual,
  * combine alone when residual is NULL (the engine's routed_up projection
  * follows it). No reference counterpart: it replaces the router, top-k,
  * host sync, expert loop and weighted sum of decode_routed_layer and
- * prefill_routed_layer. router_columns % 8 == 0 (<= 8192 for one token);
+ * prefill_routed_layer. router_columns % 8 == 0 (one token runs the decode
+ * kernels up to 8192 router columns, the batched router above that);
  * router_input and router_weight 16-byte aligned; workspace
  * k3_moe_workspace_bytes(shape, T) (the router's width does not change it).
  * Routes, workspace and alignment otherwise as k3_moe_forward_bf16.
