@@ -139,6 +139,8 @@ def cpu_baseline(cfg, inputs_cpu, store, budget_s, threads, full_tokens):
     while n < T:
         O.layer(cfg, inputs_cpu, experts, tokens=[n], threads=threads)
         n += 1
+        if n % 64 == 0:
+            log(f"bench: CPU baseline {n}/{T} tokens, {time.perf_counter() - t0:.0f} s")
         if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
@@ -283,6 +285,9 @@ def main():
     ap.add_argument("--misalign", action="store_true",
                     help="start the odd experts' tensors 8 bytes past a 16-byte boundary, as "
                          "about a quarter of a real checkpoint's tensors do")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="run the CPU baseline over every token of the batch (no time budget, "
+                         "no extrapolation; config 3 takes ~3 minutes)")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the extra HIP-graph replay figure (`graph` in the JSON line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -504,9 +509,11 @@ def run_layer(args, cfg, T, precision, steps, warmup, R, with_cpu, cpu_budget=No
         log(f"bench: CPU baseline (C oracle) for {cfg.name} ...")
         # a bounded sample of the same workload: its first tokens (for T = 1
         # the rotated decode tokens), each run through the oracle layer
-        cpu_inputs = make_inputs(cfg, tokens=min(64, max(T * R, 1)) if T > 1 else R)
+        full = getattr(args, "cpu_full", False) and T > 1
+        cpu_inputs = make_inputs(cfg, tokens=T if full else (min(64, max(T * R, 1)) if T > 1 else R))
         result["cpu_baseline"] = cpu_baseline(
-            cfg, cpu_inputs, moe.store, cpu_budget or args.cpu_budget, cpu_threads(), T)
+            cfg, cpu_inputs, moe.store, float("inf") if full else (cpu_budget or args.cpu_budget),
+            cpu_threads(), T)
     del moe, xs, rs, out, ws
     return result
 
