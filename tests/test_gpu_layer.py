@@ -304,6 +304,64 @@ def test_cfg4_full_routes_and_sample_vs_oracle(cuda, precision):
         assert (np.abs(g - f) <= lim).all()
 
 
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("precision", [0, 1], ids=["exact", "mfma"])
+def test_max_tokens_k3(cuda, precision):
+    """The largest batch the layer takes, 65535 tokens (the entry points'
+    limit; the combine's grid is one row of blocks per token, 65535 the
+    largest grid dimension), at the K3 shape with config 4's Zipf routing:
+    1,048,560 routes, per-route outputs past 2^32 elements, every tile
+    class full. The plan of all routes equals the oracle's stable-sort
+    plan; 512 sampled tokens' ids match the oracle router (near-ties as
+    O.check_routes allows) with bit-equal weights; 24 of them (some on the
+    heaviest experts) match the oracle layer bit for bit on the exact path
+    and within the MFMA tolerance on the MFMA path."""
+    cfg = CONFIGS[4]
+    T = 65535
+    inputs = make_inputs(cfg, tokens=T)
+    moe = get_layer(cfg, inputs, cuda)
+    x = L.bf16_tensor(inputs.hidden, cuda)
+    r = L.bf16_tensor(inputs.residual, cuda)
+    ids_d = torch.zeros((T, cfg.top_k), dtype=torch.int32, device=cuda)
+    w_d = torch.zeros((T, cfg.top_k), dtype=torch.float32, device=cuda)
+    out_d = moe.forward(x, r, ids=ids_d, weights=w_d, precision=precision)
+    torch.cuda.synchronize()
+    out, ids, w = L.bf16_bits(out_d), ids_d.cpu().numpy().view(np.uint32), w_d.cpu().numpy()
+    del out_d, x, r
+    c, o, u, t_i, r_i = O.route_plan(ids, cfg.experts)
+    gc, go, gu, gt, gr = plan_of(ids, cfg.experts, cuda)
+    for a, b in ((gc, c), (go, o), (gu, u), (gt, t_i), (gr, r_i)):
+        np.testing.assert_array_equal(a, b)
+    rng = np.random.default_rng(65535)
+    sample = np.sort(rng.choice(T, 512, replace=False))
+    sample[-1] = T - 1  # the last grid row
+    logits = O.router_logits(inputs.router_weight, inputs.hidden[sample])
+    bad = O.check_routes(ids[sample], w[sample], logits, inputs.router_bias, cfg.top_k, cfg.scale)
+    heavy = np.argsort(-c, kind="stable")[:3]
+    print(f"\nT={T}: U = {u.size}, heaviest experts {heavy.tolist()} with {c[heavy].tolist()} rows; "
+          f"{bad.size}/512 sampled tokens near-ties")
+    picks = {int(T - 1), 0}
+    for e in heavy:
+        rows = t_i[o[e]:o[e + 1]]
+        picks.update(rng.choice(rows, 3, replace=False).tolist())
+    picks.update(int(sample[t]) for t in bad)
+    picks.update(rng.choice(sample, 24 - len(picks), replace=False).tolist())
+    tokens = np.array(sorted(picks), dtype=np.uint32)
+    if precision == 0:
+        check_tokens(cfg, inputs, moe.store, out, ids, w, tokens)
+    else:
+        want = O.layer(cfg, inputs, host_experts(moe.store, ids[tokens]), tokens=tokens, ids=ids,
+                       weights=w)
+        g = bf16_bits_to_f32(out[tokens]).astype(np.float64)
+        f = bf16_bits_to_f32(want["output"]).astype(np.float64)
+        rel = np.linalg.norm(g - f) / np.linalg.norm(f)
+        rms = np.sqrt(np.mean(f * f))
+        lim = 4 * 2.0 ** (np.floor(np.log2(np.maximum(np.abs(f), rms))) - 7)
+        print(f"T={T} MFMA vs oracle on {tokens.size} tokens: rel-L2 {rel:.3g}")
+        assert rel <= 2e-3
+        assert (np.abs(g - f) <= lim).all()
+
+
 def test_expert_stage_on_given_routes(cuda):
     cfg = CONFIGS[0]
     T = 9
